@@ -1,0 +1,189 @@
+/*
+ * redpanda_hip.h — C ABI of the MI355X (gfx950) kernels for ChessMamba's
+ * hot path: the Mamba-3 exponential-trapezoidal selective scan (forward,
+ * bidirectional forward, analytic reverse-scan backward) and the batched
+ * O(1) recurrent step.
+ *
+ * Plain C: device pointers, element counts and strides, a hipStream_t passed
+ * as void*.  The library never allocates or frees device memory; every buffer
+ * (outputs and workspace) is caller-allocated, as the reference allocates its
+ * outputs and scratch with torch (engine/triton_scan.py:260-262, :293-300).
+ * All entry points are asynchronous on the given stream and return 0 or a
+ * negative status; rp_last_error() describes the last failure of the calling
+ * thread.  Nothing blocks, nothing aborts, no exceptions cross the ABI.
+ *
+ * Recurrence (one channel d, state index n; NR rotational + NT tracking):
+ *   g_t[n]    = exp(dt_t Ar[d,n]) cos(dt_t Ai[d,n])   n <  NR
+ *             = Tk[d,n-NR]  (= tanh theta)            n >= NR
+ *   beta_t[n] = dt_t u_t B_t[n]
+ *   h_t       = g_t h_{t-1} + beta_t/2 + g_t beta_{t-1}/2
+ *   y_t       = sum_n h_t[n] C_t[n]           (scan: no D-skip; step: + u D)
+ */
+#ifndef REDPANDA_HIP_H
+#define REDPANDA_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RP_ABI_VERSION 1
+
+/* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
+ * tensor carries its own code, as autocast hands over mixed dtypes */
+enum { RP_F32 = 0, RP_BF16 = 1, RP_F16 = 2 };
+
+/* status codes */
+enum {
+  RP_OK = 0,
+  RP_ERR_INVALID = -1,      /* bad shape, stride, pointer or dtype   */
+  RP_ERR_UNSUPPORTED = -2,  /* a size beyond the compiled limits     */
+  RP_ERR_LAUNCH = -3,       /* hipGetLastError after a launch        */
+  RP_ERR_WORKSPACE = -4     /* workspace missing or too small        */
+};
+
+/* Largest supported state dimension N = NR + NT. */
+#define RP_MAX_STATE 128
+
+/*
+ * Scan arguments.  delta, u: (B, L, D); Bc, Cc: (B, L, N) — B and C already
+ * contracted over the MIMO dimension p (engine/mamba.py:336-337).  Strides
+ * are in elements for the batch and time dimensions; the innermost (channel
+ * or state) stride must be 1.  A_real, A_imag: (D, NR) fp32 row-major, or
+ * NULL; A_imag NULL means a real decay gate exp(dt Ar).  track: (D, NT) fp32
+ * tanh(theta) gates, or NULL when NT == 0.  h0, beta0: NULL (zero state, as
+ * the reference's scan always starts), or (B, D, N) fp32 contiguous state to
+ * continue from — the cache format of step() (causal scans, L >= 1).
+ */
+typedef struct rp_scan_args {
+  int64_t B, L, D, N, NR, NT;
+  int32_t dtype_delta, dtype_u, dtype_B, dtype_C;  /* RP_F32 / RP_BF16 / RP_F16 */
+  int32_t bidirectional;   /* 0: causal; 1: y = S(x) + flip(S(flip(x)))     */
+  int32_t reserved;        /* must be 0 */
+  const void* delta;  int64_t delta_sb, delta_sl;
+  const void* u;      int64_t u_sb, u_sl;
+  const void* Bc;     int64_t Bc_sb, Bc_sl;
+  const void* Cc;     int64_t Cc_sb, Cc_sl;
+  const float* A_real;
+  const float* A_imag;
+  const float* track;
+  const float* h0;
+  const float* beta0;
+} rp_scan_args;
+
+/*
+ * Forward outputs.  y: (B, L, D) fp32 contiguous, WITHOUT the u*D skip
+ * (the caller adds it, as engine/mamba.py:350 does).  ckpt: NULL for
+ * inference, else rp_scan_ckpt_bytes() of workspace that rp_scan_bwd reads.
+ * h_last, beta_last: NULL, or (B, D, N) fp32 contiguous to receive the final
+ * recurrent state (h_{L-1}, beta_{L-1}) that rp_step continues from
+ * (engine/mamba.py:377-379); causal scans only.
+ */
+typedef struct rp_scan_fwd_out {
+  float* y;
+  float* ckpt;
+  float* h_last;
+  float* beta_last;
+} rp_scan_fwd_out;
+
+/*
+ * Backward.  dy: (B, L, D) fp32 contiguous upstream gradient of y.  ckpt:
+ * the workspace the matching forward filled.  Outputs, fp32 contiguous:
+ * d_delta, d_u (B, L, D); d_Bc, d_Cc (B, L, N); d_A_real, d_A_imag (D, NR)
+ * (d_A_imag ignored when A_imag is NULL); d_track (D, NT).  work:
+ * rp_scan_bwd_work_bytes() of scratch.  dh_last, dbeta_last: NULL, or
+ * (B, D, N) fp32 gradients of the final state returned by a causal forward
+ * (training through prime_cache + step, engine/search_mamba.py:252-273).
+ * d_h0, d_beta0: NULL, or (B, D, N) fp32 outputs receiving the gradient of
+ * the initial state h0 / beta0 (requires h0).  Deterministic: no float
+ * atomics.
+ */
+typedef struct rp_scan_bwd_io {
+  const float* dy;
+  const float* ckpt;
+  const float* dh_last;
+  const float* dbeta_last;
+  float* d_delta;
+  float* d_u;
+  float* d_Bc;
+  float* d_Cc;
+  float* d_A_real;
+  float* d_A_imag;
+  float* d_track;
+  float* d_h0;
+  float* d_beta0;
+  void* work;
+  int64_t work_bytes;
+} rp_scan_bwd_io;
+
+/*
+ * Step arguments (one token per rollout, engine/mamba.py:466-498).
+ * delta, u: (R, D) fp32 with row stride; Bc, Cc: (R, N) fp32 with row
+ * stride; h_in, beta_in: (R, D, N) fp32 contiguous, or both NULL for a fresh
+ * (zero) state; Dskip: (D,) fp32.  Outputs: h_out, beta_out (R, D, N) fp32
+ * contiguous (may alias h_in / beta_in for an in-place update); y: (R, D)
+ * fp32 contiguous = sum_n h_out C + u D.  beta_out = (dt u) B exactly as the
+ * reference stores dBu_t.
+ */
+typedef struct rp_step_args {
+  int64_t R, D, N, NR, NT;
+  const float* delta;  int64_t delta_sr;
+  const float* u;      int64_t u_sr;
+  const float* Bc;     int64_t Bc_sr;
+  const float* Cc;     int64_t Cc_sr;
+  const float* h_in;
+  const float* beta_in;
+  const float* A_real;
+  const float* A_imag;
+  const float* track;
+  const float* Dskip;
+  float* h_out;
+  float* beta_out;
+  float* y;
+} rp_step_args;
+
+/* ABI version this library was built with (RP_ABI_VERSION). */
+int rp_abi_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* rp_last_error(void);
+
+/* Validate scan arguments on the host without launching anything. */
+int rp_scan_check(const rp_scan_args* a);
+
+/* Bytes of checkpoint workspace rp_scan_fwd writes for a later backward. */
+int64_t rp_scan_ckpt_bytes(const rp_scan_args* a);
+
+/* Bytes of scratch rp_scan_bwd needs. */
+int64_t rp_scan_bwd_work_bytes(const rp_scan_args* a);
+
+/*
+ * Forward scan; replaces _TrapezoidalScanFn.forward / _fwd_kernel
+ * (engine/triton_scan.py:247-281, :44-98) and, with bidirectional = 1, the
+ * two-pass bidirectional branch of Mamba3Block.forward
+ * (engine/mamba.py:254-260, minus the D-skip).
+ */
+int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream);
+
+/*
+ * Analytic backward; replaces _TrapezoidalScanFn.backward / _bwd_kernel
+ * (engine/triton_scan.py:283-315, :100-241) including the dBp/dCp partial
+ * sums and the dA atomics, here as deterministic two-stage reductions.
+ */
+int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream);
+
+/* Validate step arguments on the host without launching anything. */
+int rp_step_check(const rp_step_args* a);
+
+/*
+ * Fused O(1) step of the SSM core; replaces the ~20 torch ops of
+ * Mamba3Block.step between the projections (engine/mamba.py:466-494).
+ */
+int rp_step(const rp_step_args* a, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REDPANDA_HIP_H */

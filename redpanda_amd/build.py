@@ -1,0 +1,91 @@
+"""Build libredpanda_hip.so in-tree with hipcc for gfx950.
+
+    python -m redpanda_amd.build [--verbose]
+
+Compiles every .hip file under redpanda_amd/csrc/ to an object in parallel,
+then links one shared library next to this file.  The library links the HIP
+runtime that torch ships (same soname, resolved through an rpath to torch's
+lib directory), so torch's streams are valid handles inside it.
+"""
+
+import os
+import subprocess
+import sys
+import sysconfig
+import tempfile
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB_NAME = "libredpanda_hip.so"
+LIB_PATH = os.path.join(HERE, LIB_NAME)
+ARCH = "gfx950"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# Device-code flags.  -ffp-contract=off: every FMA is written out explicitly,
+# so the scan and step kernels round identically.  Packed-FP32 instructions
+# are disabled for the device.
+DEVICE_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-mcode-object-version=5", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _torch_lib_dir():
+    try:
+        import torch  # noqa: F401
+        return os.path.join(os.path.dirname(torch.__file__), "lib")
+    except Exception:  # pragma: no cover - torch is part of the image
+        return os.path.join(sysconfig.get_paths()["purelib"], "torch", "lib")
+
+
+def sources():
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build(verbose=False, extra_flags=()):
+    """Compile and link; returns the library path.  Raises on any failure."""
+    srcs = sources()
+    tmp = tempfile.mkdtemp(prefix="rp_build_")
+    objs, procs = [], []
+    for src in srcs:
+        obj = os.path.join(tmp, os.path.basename(src) + ".o")
+        cmd = [HIPCC, *DEVICE_FLAGS, *extra_flags, "-I", INCLUDE, "-I", CSRC, "-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
+        objs.append(obj)
+    failed = []
+    for src, pr in procs:
+        out, _ = pr.communicate()
+        text = out.decode(errors="replace")
+        # the host pass does not know the device-only target feature: harmless
+        text = "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l)
+        if pr.returncode != 0:
+            failed.append((src, text))
+        elif verbose and text.strip():
+            print(text)
+    if failed:
+        msg = "\n".join(f"--- {s}\n{t}" for s, t in failed)
+        raise RuntimeError(f"hipcc failed:\n{msg}")
+    tl = _torch_lib_dir()
+    tmp_lib = LIB_PATH + ".tmp"
+    link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib,
+            "-L", tl, "-Wl,-rpath," + tl, "-Wl,--no-undefined"]
+    if verbose:
+        print(" ".join(link), flush=True)
+    res = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+    if res.returncode != 0:
+        raise RuntimeError("link failed:\n" + res.stdout.decode(errors="replace"))
+    os.replace(tmp_lib, LIB_PATH)
+    for o in objs:
+        os.remove(o)
+    os.rmdir(tmp)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="--verbose" in sys.argv))

@@ -1,0 +1,372 @@
+// extern "C" boundary of libredpanda_hip: argument validation, workspace
+// sizing, shape selection and launches.  No allocation, no blocking, no
+// exceptions; failures return a negative status and set a thread-local
+// message (rp_last_error).
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "redpanda_hip.h"
+#include "rp_launch.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int fail_hip(hipError_t e, const char* what) {
+  return fail(RP_ERR_LAUNCH, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+constexpr int64_t kI32Max = 0x7fffffff;
+
+bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t elem_size(int dtype) { return dtype == RP_F32 ? 4 : 2; }
+
+int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+
+// Lanes-per-channel override for tuning (RP_LANES_PER_CHANNEL=4 or 8).
+int lanes_override() {
+  static int v = [] {
+    const char* s = getenv("RP_LANES_PER_CHANNEL");
+    if (s == nullptr) return 0;
+    const int x = atoi(s);
+    return (x == 4 || x == 8) ? x : 0;
+  }();
+  return v;
+}
+
+struct Plan {
+  int S, NPL, CB, ntiles, nck, ndir, bg, nbg;
+  int64_t ckpt_bytes, part_bc_bytes, part_par_bytes;
+};
+
+int scan_validate(const rp_scan_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "scan args: NULL");
+  if (a->B < 0 || a->L < 0 || a->D < 0 || a->NR < 0 || a->NT < 0)
+    return fail(RP_ERR_INVALID, "scan args: negative size (B=%lld L=%lld D=%lld NR=%lld NT=%lld)",
+                (long long)a->B, (long long)a->L, (long long)a->D, (long long)a->NR,
+                (long long)a->NT);
+  if (a->N != a->NR + a->NT)
+    return fail(RP_ERR_INVALID, "scan args: N=%lld must equal NR+NT=%lld", (long long)a->N,
+                (long long)(a->NR + a->NT));
+  if (a->N < 1 || a->N > RP_MAX_STATE)
+    return fail(RP_ERR_UNSUPPORTED, "scan args: N=%lld outside [1, %d]", (long long)a->N,
+                RP_MAX_STATE);
+  if (a->B > kI32Max || a->L > kI32Max || a->D > kI32Max)
+    return fail(RP_ERR_UNSUPPORTED, "scan args: B, L, D must each fit in int32");
+  const int codes[4] = {a->dtype_delta, a->dtype_u, a->dtype_B, a->dtype_C};
+  for (int code : codes)
+    if (code != RP_F32 && code != RP_BF16 && code != RP_F16)
+      return fail(RP_ERR_INVALID, "scan args: unknown dtype code %d", code);
+  if (a->reserved != 0) return fail(RP_ERR_INVALID, "scan args: reserved field must be 0");
+  if (a->bidirectional != 0 && a->bidirectional != 1)
+    return fail(RP_ERR_INVALID, "scan args: bidirectional must be 0 or 1");
+  const int64_t work = a->B * a->L;
+  if (work > 0 && a->D > 0) {
+    if (!a->delta || !a->u || !a->Bc || !a->Cc)
+      return fail(RP_ERR_INVALID, "scan args: NULL delta/u/Bc/Cc");
+    if (!aligned(a->delta, elem_size(a->dtype_delta)) || !aligned(a->u, elem_size(a->dtype_u)) ||
+        !aligned(a->Bc, elem_size(a->dtype_B)) || !aligned(a->Cc, elem_size(a->dtype_C)))
+      return fail(RP_ERR_INVALID, "scan args: misaligned input pointer");
+    if (a->delta_sb < 0 || a->delta_sl < 0 || a->u_sb < 0 || a->u_sl < 0 || a->Bc_sb < 0 ||
+        a->Bc_sl < 0 || a->Cc_sb < 0 || a->Cc_sl < 0)
+      return fail(RP_ERR_INVALID, "scan args: negative stride");
+  }
+  if (a->D > 0) {
+    if (a->NR > 0 && (!a->A_real || !aligned(a->A_real, 4)))
+      return fail(RP_ERR_INVALID, "scan args: NR>0 needs a 4-byte aligned A_real");
+    if (a->NR > 0 && a->A_imag && !aligned(a->A_imag, 4))
+      return fail(RP_ERR_INVALID, "scan args: misaligned A_imag");
+    if (a->NR == 0 && a->A_imag)
+      return fail(RP_ERR_INVALID, "scan args: A_imag given without rotational states");
+    if (a->NT > 0 && (!a->track || !aligned(a->track, 4)))
+      return fail(RP_ERR_INVALID, "scan args: NT>0 needs a 4-byte aligned track");
+  }
+  if ((a->h0 == nullptr) != (a->beta0 == nullptr))
+    return fail(RP_ERR_INVALID, "scan args: h0 and beta0 go together");
+  if (a->h0 != nullptr) {
+    if (a->bidirectional)
+      return fail(RP_ERR_INVALID, "scan args: an initial state needs a causal scan");
+    if (a->L < 1) return fail(RP_ERR_INVALID, "scan args: an initial state needs L >= 1");
+    if (!aligned(a->h0, 4) || !aligned(a->beta0, 4))
+      return fail(RP_ERR_INVALID, "scan args: misaligned initial state");
+  }
+  return RP_OK;
+}
+
+Plan make_plan(const rp_scan_args* a) {
+  Plan pl{};
+  int S = 0, NPL = 0;
+  rp::choose_shape((int)a->N, &S, &NPL);
+  pl.S = S;
+  pl.NPL = NPL;
+  pl.CB = rp::kWaves * (rp::kWave / S);
+  pl.ntiles = (int)((a->D + pl.CB - 1) / pl.CB);
+  const int64_t nchunks = (a->L + rp::kCkptK - 1) / rp::kCkptK;
+  pl.nck = (int)(nchunks > 0 ? nchunks - 1 : 0);
+  pl.ndir = a->bidirectional ? 2 : 1;
+  // batch rows per backward workgroup: enough workgroups to fill 256 CUs
+  // several times over, while amortising the parameter-gradient partials
+  int64_t bg = (a->B * (int64_t)pl.ntiles) / 2048;
+  if (bg < 1) bg = 1;
+  if (bg > 8) bg = 8;
+  pl.bg = (int)bg;
+  pl.nbg = (int)((a->B + bg - 1) / bg);
+  pl.ckpt_bytes = (int64_t)pl.ndir * a->B * pl.nck * pl.ntiles * rp::kThreads * NPL * 4;
+  pl.part_bc_bytes = round_up(2 * (int64_t)pl.ntiles * a->B * a->L * a->N * 4, 256);
+  pl.part_par_bytes = round_up((int64_t)pl.nbg * 2 * a->D * a->N * 4, 256);
+  return pl;
+}
+
+rp::ScanParams scan_params(const rp_scan_args* a, const Plan& pl) {
+  rp::ScanParams p{};
+  p.delta = a->delta;
+  p.u = a->u;
+  p.Bc = a->Bc;
+  p.Cc = a->Cc;
+  p.dsb = a->delta_sb;
+  p.dsl = a->delta_sl;
+  p.usb = a->u_sb;
+  p.usl = a->u_sl;
+  p.bsb = a->Bc_sb;
+  p.bsl = a->Bc_sl;
+  p.csb = a->Cc_sb;
+  p.csl = a->Cc_sl;
+  p.Ar = a->NR > 0 ? a->A_real : nullptr;
+  p.Ai = a->NR > 0 ? a->A_imag : nullptr;
+  p.Tk = a->NT > 0 ? a->track : nullptr;
+  p.h0 = a->h0;
+  p.beta0 = a->beta0;
+  p.B = (int)a->B;
+  p.L = (int)a->L;
+  p.D = (int)a->D;
+  p.N = (int)a->N;
+  p.NR = (int)a->NR;
+  p.NT = (int)a->NT;
+  p.dt_delta = a->dtype_delta;
+  p.dt_u = a->dtype_u;
+  p.dt_B = a->dtype_B;
+  p.dt_C = a->dtype_C;
+  p.ndir = pl.ndir;
+  p.ntiles = pl.ntiles;
+  p.nck = pl.nck;
+  return p;
+}
+
+}  // namespace
+
+namespace rp {
+
+bool choose_shape(int N, int* S, int* NPL) {
+  static const int npl4[] = {1, 2, 3, 4, 5, 6, 8, 10};
+  static const int npl8[] = {6, 8, 9, 10, 12, 16};
+  const int force = lanes_override();
+  if (N <= 40 && force != 8) {
+    for (int v : npl4)
+      if (4 * v >= N) {
+        *S = 4;
+        *NPL = v;
+        return true;
+      }
+  }
+  for (int v : npl8)
+    if (8 * v >= N) {
+      *S = 8;
+      *NPL = v;
+      return true;
+    }
+  return false;
+}
+
+}  // namespace rp
+
+extern "C" {
+
+int rp_abi_version(void) { return RP_ABI_VERSION; }
+
+const char* rp_last_error(void) { return g_err; }
+
+int rp_scan_check(const rp_scan_args* a) { return scan_validate(a); }
+
+int64_t rp_scan_ckpt_bytes(const rp_scan_args* a) {
+  if (scan_validate(a) != RP_OK) return -1;
+  return make_plan(a).ckpt_bytes;
+}
+
+int64_t rp_scan_bwd_work_bytes(const rp_scan_args* a) {
+  if (scan_validate(a) != RP_OK) return -1;
+  const Plan pl = make_plan(a);
+  return pl.part_bc_bytes + pl.part_par_bytes;
+}
+
+int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream) {
+  int st = scan_validate(a);
+  if (st != RP_OK) return st;
+  if (out == nullptr) return fail(RP_ERR_INVALID, "scan fwd: NULL output block");
+  const int64_t work = a->B * a->L * a->D;
+  if (work > 0 && (!out->y || !aligned(out->y, 4)))
+    return fail(RP_ERR_INVALID, "scan fwd: NULL or misaligned y");
+  if ((out->h_last == nullptr) != (out->beta_last == nullptr))
+    return fail(RP_ERR_INVALID, "scan fwd: h_last and beta_last go together");
+  if (out->h_last && a->bidirectional)
+    return fail(RP_ERR_INVALID, "scan fwd: the final state exists for causal scans only");
+  const Plan pl = make_plan(a);
+  if (out->ckpt && pl.ckpt_bytes > 0 && !aligned(out->ckpt, 4))
+    return fail(RP_ERR_INVALID, "scan fwd: misaligned checkpoint workspace");
+  if (a->B == 0 || a->D == 0) return RP_OK;
+  if (a->L == 0) {
+    if (out->h_last) {
+      const int64_t ne = a->B * a->D * a->N;
+      hipError_t e = rp::launch_fill_zero(out->h_last, ne, (hipStream_t)stream);
+      if (e == hipSuccess) e = rp::launch_fill_zero(out->beta_last, ne, (hipStream_t)stream);
+      if (e != hipSuccess) return fail_hip(e, "scan fwd: zero final state");
+    }
+    return RP_OK;
+  }
+  if ((int64_t)pl.ntiles * a->B > kI32Max)
+    return fail(RP_ERR_UNSUPPORTED, "scan fwd: grid too large");
+  const rp::ScanParams p = scan_params(a, pl);
+  rp::FwdOut o{out->y, pl.ckpt_bytes > 0 ? out->ckpt : nullptr, out->h_last, out->beta_last};
+  hipError_t e = rp::launch_scan_fwd(pl.S, pl.NPL, p, o, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "scan fwd launch");
+  return RP_OK;
+}
+
+int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
+  int st = scan_validate(a);
+  if (st != RP_OK) return st;
+  if (io == nullptr) return fail(RP_ERR_INVALID, "scan bwd: NULL io block");
+  const Plan pl = make_plan(a);
+  const int64_t need = pl.part_bc_bytes + pl.part_par_bytes;
+  const int64_t work = a->B * a->L * a->D;
+  if (work > 0) {
+    if (!io->dy || !io->d_delta || !io->d_u)
+      return fail(RP_ERR_INVALID, "scan bwd: NULL dy / d_delta / d_u");
+    if (pl.ckpt_bytes > 0 && !io->ckpt)
+      return fail(RP_ERR_INVALID, "scan bwd: checkpoint workspace required for L=%lld",
+                  (long long)a->L);
+  }
+  if (a->B * a->L > 0 && (!io->d_Bc || !io->d_Cc))
+    return fail(RP_ERR_INVALID, "scan bwd: NULL d_Bc / d_Cc");
+  if (a->D > 0) {
+    if (a->NR > 0 && !io->d_A_real) return fail(RP_ERR_INVALID, "scan bwd: NULL d_A_real");
+    if (a->NR > 0 && a->A_imag && !io->d_A_imag)
+      return fail(RP_ERR_INVALID, "scan bwd: NULL d_A_imag");
+    if (a->NT > 0 && !io->d_track) return fail(RP_ERR_INVALID, "scan bwd: NULL d_track");
+  }
+  if ((io->d_h0 == nullptr) != (io->d_beta0 == nullptr))
+    return fail(RP_ERR_INVALID, "scan bwd: d_h0 and d_beta0 go together");
+  if (io->d_h0 && !a->h0)
+    return fail(RP_ERR_INVALID, "scan bwd: d_h0 needs an initial state h0");
+  if ((io->dh_last || io->dbeta_last) && a->bidirectional)
+    return fail(RP_ERR_INVALID, "scan bwd: final-state gradients exist for causal scans only");
+  if (need > 0 && (io->work == nullptr || io->work_bytes < need || !aligned(io->work, 256)))
+    return fail(RP_ERR_WORKSPACE, "scan bwd: workspace needs %lld bytes (256-aligned), got %lld",
+                (long long)need, (long long)io->work_bytes);
+  if (a->D == 0) return RP_OK;
+  if ((int64_t)pl.ntiles * pl.nbg > kI32Max)
+    return fail(RP_ERR_UNSUPPORTED, "scan bwd: grid too large");
+  const rp::ScanParams p = scan_params(a, pl);
+  rp::BwdIO b{};
+  b.dy = io->dy;
+  b.ckpt = io->ckpt;
+  b.dh_last = io->dh_last;
+  b.dbeta_last = io->dbeta_last;
+  b.d_h0 = io->d_h0;
+  b.d_beta0 = io->d_beta0;
+  b.d_delta = io->d_delta;
+  b.d_u = io->d_u;
+  b.part_bc = static_cast<float*>(io->work);
+  b.part_par = reinterpret_cast<float*>(static_cast<char*>(io->work) + pl.part_bc_bytes);
+  b.bg = pl.bg;
+  b.nbg = pl.nbg;
+  hipStream_t s = (hipStream_t)stream;
+  if (a->B > 0) {
+    hipError_t e = rp::launch_scan_bwd(pl.S, pl.NPL, p, b, s);
+    if (e != hipSuccess) return fail_hip(e, "scan bwd launch");
+  }
+  hipError_t e = rp::launch_bwd_finalize(p, b, io->d_Bc, io->d_Cc,
+                                         a->NR > 0 ? io->d_A_real : nullptr,
+                                         (a->NR > 0 && a->A_imag) ? io->d_A_imag : nullptr,
+                                         a->NT > 0 ? io->d_track : nullptr, s);
+  if (e != hipSuccess) return fail_hip(e, "scan bwd finalize launch");
+  return RP_OK;
+}
+
+int rp_step_check(const rp_step_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "step args: NULL");
+  if (a->R < 0 || a->D < 0 || a->NR < 0 || a->NT < 0)
+    return fail(RP_ERR_INVALID, "step args: negative size");
+  if (a->N != a->NR + a->NT) return fail(RP_ERR_INVALID, "step args: N must equal NR+NT");
+  if (a->N < 1 || a->N > RP_MAX_STATE)
+    return fail(RP_ERR_UNSUPPORTED, "step args: N=%lld outside [1, %d]", (long long)a->N,
+                RP_MAX_STATE);
+  if (a->R > kI32Max || a->D > kI32Max)
+    return fail(RP_ERR_UNSUPPORTED, "step args: R and D must fit in int32");
+  if (a->R == 0 || a->D == 0) return RP_OK;
+  if (!a->delta || !a->u || !a->Bc || !a->Cc || !a->Dskip || !a->h_out || !a->beta_out || !a->y)
+    return fail(RP_ERR_INVALID, "step args: NULL required pointer");
+  if ((a->h_in == nullptr) != (a->beta_in == nullptr))
+    return fail(RP_ERR_INVALID, "step args: h_in and beta_in go together");
+  if (a->NR > 0 && !a->A_real) return fail(RP_ERR_INVALID, "step args: NR>0 needs A_real");
+  if (a->NR == 0 && a->A_imag) return fail(RP_ERR_INVALID, "step args: A_imag without NR");
+  if (a->NT > 0 && !a->track) return fail(RP_ERR_INVALID, "step args: NT>0 needs track");
+  if (a->delta_sr < a->D || a->u_sr < a->D || a->Bc_sr < a->N || a->Cc_sr < a->N)
+    return fail(RP_ERR_INVALID, "step args: row stride shorter than the row");
+  const void* ptrs[] = {a->delta, a->u, a->Bc, a->Cc, a->h_in, a->beta_in, a->A_real,
+                        a->A_imag, a->track, a->Dskip, a->h_out, a->beta_out, a->y};
+  for (const void* q : ptrs)
+    if (q && !aligned(q, 4)) return fail(RP_ERR_INVALID, "step args: misaligned pointer");
+  return RP_OK;
+}
+
+int rp_step(const rp_step_args* a, void* stream) {
+  int st = rp_step_check(a);
+  if (st != RP_OK) return st;
+  if (a->R == 0 || a->D == 0) return RP_OK;
+  int S = 0, NPL = 0;
+  rp::choose_shape((int)a->N, &S, &NPL);
+  const int CB = rp::kWaves * (rp::kWave / S);
+  rp::StepParams p{};
+  p.R = (int)a->R;
+  p.D = (int)a->D;
+  p.N = (int)a->N;
+  p.NR = (int)a->NR;
+  p.NT = (int)a->NT;
+  p.delta = a->delta;
+  p.dsr = a->delta_sr;
+  p.u = a->u;
+  p.usr = a->u_sr;
+  p.Bc = a->Bc;
+  p.bsr = a->Bc_sr;
+  p.Cc = a->Cc;
+  p.csr = a->Cc_sr;
+  p.h_in = a->h_in;
+  p.beta_in = a->beta_in;
+  p.Ar = a->NR > 0 ? a->A_real : nullptr;
+  p.Ai = a->NR > 0 ? a->A_imag : nullptr;
+  p.Tk = a->NT > 0 ? a->track : nullptr;
+  p.Dskip = a->Dskip;
+  p.h_out = a->h_out;
+  p.beta_out = a->beta_out;
+  p.y = a->y;
+  p.ntiles = (int)((a->D + CB - 1) / CB);
+  if ((int64_t)p.ntiles * a->R > kI32Max)
+    return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
+  hipError_t e = rp::launch_step(S, NPL, p, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "step launch");
+  return RP_OK;
+}
+
+}  // extern "C"

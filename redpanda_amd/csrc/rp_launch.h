@@ -1,0 +1,97 @@
+// Kernel parameter blocks and host-side launchers (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rp {
+
+constexpr int kWave = 64;
+constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kThreads = kWave * kWaves;
+
+// Time steps staged in LDS per block by the forward and backward kernels,
+// and the checkpoint interval of the backward's recompute.
+constexpr int kFwdTB = 32;
+constexpr int kBwdTB = 16;
+constexpr int kCkptK = 8;
+
+struct ScanParams {
+  const void* delta;
+  const void* u;
+  const void* Bc;
+  const void* Cc;
+  int64_t dsb, dsl, usb, usl, bsb, bsl, csb, csl;
+  const float* Ar;
+  const float* Ai;
+  const float* Tk;
+  const float* h0;     // (B, D, N) initial state or null (zero)
+  const float* beta0;
+  int B, L, D, N, NR, NT;
+  int dt_delta, dt_u, dt_B, dt_C;
+  int ndir;      // 1 causal, 2 bidirectional
+  int ntiles;    // ceil(D / CB)
+  int nck;       // stored checkpoints per (dir, b): ceil(L / K) - 1
+};
+
+struct FwdOut {
+  float* y;
+  float* ckpt;
+  float* h_last;
+  float* beta_last;
+};
+
+struct BwdIO {
+  const float* dy;
+  const float* ckpt;
+  const float* dh_last;     // (B, D, N) or null: gradient of the final h
+  const float* dbeta_last;  // (B, D, N) or null: gradient of the final beta
+  float* d_delta;
+  float* d_u;
+  float* d_h0;       // (B, D, N) or null
+  float* d_beta0;
+  float* part_bc;   // [2][ntiles][B][L][N]  per-tile dB / dC partial sums
+  float* part_par;  // [nbg][2][D][N]        per-batch-group dA partial sums
+  int bg;           // batch rows per workgroup
+  int nbg;          // ceil(B / bg)
+};
+
+struct StepParams {
+  int R, D, N, NR, NT;
+  const float* delta;
+  int64_t dsr;
+  const float* u;
+  int64_t usr;
+  const float* Bc;
+  int64_t bsr;
+  const float* Cc;
+  int64_t csr;
+  const float* h_in;
+  const float* beta_in;
+  const float* Ar;
+  const float* Ai;
+  const float* Tk;
+  const float* Dskip;
+  float* h_out;
+  float* beta_out;
+  float* y;
+  int ntiles;
+};
+
+// Chosen lane split for a state dimension N: S lanes per channel holding NPL
+// states each.  Returns false when N is beyond the compiled shapes.
+bool choose_shape(int N, int* S, int* NPL);
+
+hipError_t launch_scan_fwd(int S, int NPL, const ScanParams& p, const FwdOut& o, hipStream_t st);
+hipError_t launch_scan_bwd(int S, int NPL, const ScanParams& p, const BwdIO& io, hipStream_t st);
+hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
+                               float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st);
+hipError_t launch_step(int S, int NPL, const StepParams& p, hipStream_t st);
+hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
+
+}  // namespace rp
+
+// Compiled (S, NPL) shapes: S lanes per channel, NPL states per lane.
+#define RP_FOR_EACH_SHAPE(X) \
+  X(4, 1) X(4, 2) X(4, 3) X(4, 4) X(4, 5) X(4, 6) X(4, 8) X(4, 10) \
+  X(8, 6) X(8, 8) X(8, 9) X(8, 10) X(8, 12) X(8, 16)

@@ -1,0 +1,74 @@
+"""Fused O(1) recurrent step of the SSM core (one token for a batch of rollouts).
+
+`hip_step` replaces the torch ops of Mamba3Block.step between the input
+projections and out_proj (engine/mamba.py:466-494) with one kernel that reads
+the (h, beta) state once and writes the new state once.  The new state is a
+pair of fresh tensors, as in the reference (callers clone / cat / expand cached
+states, engine/mars_search.py:222-224, engine/search_mamba.py:177-187), unless
+`out` passes preallocated (possibly aliasing) buffers.
+"""
+
+import ctypes
+
+import torch
+
+from redpanda_amd import _lib
+
+
+def _f32c(t):
+    return t.to(torch.float32).contiguous()
+
+
+def _rows(t):
+    t = t.to(torch.float32)
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None):
+    """One step for R rollouts.
+
+    delta, u: (R, D); Bc, Cc: (R, N) (contracted over p); A_real/A_imag:
+    (D, NR) or None; track: (D, NT) or None; Dskip: (D,); state: (h, beta)
+    fp32 (R, D, N) or None for a fresh state.  Returns (y (R, D) incl. u*D,
+    (h_new, beta_new)).
+    """
+    lib = _lib.load()
+    R, D = u.shape
+    N = Bc.shape[-1]
+    NR = 0 if A_real is None else A_real.shape[-1]
+    NT = 0 if track is None else track.shape[-1]
+    if NR + NT != N:
+        raise ValueError(f"step: n_rot ({NR}) + n_track ({NT}) != d_state ({N})")
+    if delta.shape != (R, D) or Bc.shape != (R, N) or Cc.shape != (R, N):
+        raise ValueError("step: delta/u must be (R, D) and B/C (R, N)")
+    dev = u.device
+    delta, u, Bc, Cc = (_rows(t) for t in (delta, u, Bc, Cc))
+    Ar = None if A_real is None else _f32c(A_real.detach())
+    Ai = None if A_imag is None else _f32c(A_imag.detach())
+    Tk = None if track is None else _f32c(track.detach())
+    Dk = _f32c(Dskip.detach())
+    h_in = beta_in = None
+    if state is not None:
+        h_in, beta_in = state
+        if h_in.shape != (R, D, N) or beta_in.shape != (R, D, N):
+            raise ValueError(f"step: state must be (R, D, N) = {(R, D, N)}")
+        h_in = _f32c(h_in)
+        beta_in = _f32c(beta_in)
+    if out is None:
+        h_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
+        beta_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
+        y = torch.empty((R, D), dtype=torch.float32, device=dev)
+    else:
+        y, h_out, beta_out = out
+    a = _lib.StepArgs()
+    a.R, a.D, a.N, a.NR, a.NT = R, D, N, NR, NT
+    a.delta, a.delta_sr = delta.data_ptr(), delta.stride(0)
+    a.u, a.u_sr = u.data_ptr(), u.stride(0)
+    a.Bc, a.Bc_sr = Bc.data_ptr(), Bc.stride(0)
+    a.Cc, a.Cc_sr = Cc.data_ptr(), Cc.stride(0)
+    a.h_in, a.beta_in = _lib.ptr(h_in), _lib.ptr(beta_in)
+    a.A_real, a.A_imag, a.track = _lib.ptr(Ar), _lib.ptr(Ai), _lib.ptr(Tk)
+    a.Dskip = Dk.data_ptr()
+    a.h_out, a.beta_out, a.y = h_out.data_ptr(), beta_out.data_ptr(), y.data_ptr()
+    _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
+    return y, (h_out, beta_out)

@@ -1,0 +1,68 @@
+"""Direct C-ABI calls for the GPU parity tests (fp32 outputs, no autograd).
+
+The product's autograd wrapper returns gradients in each input's dtype, as the
+reference does; parity of the kernels themselves is measured on the fp32
+buffers the C ABI writes, whatever the storage dtype of the inputs.
+"""
+
+import ctypes
+
+import torch
+
+from redpanda_amd import _lib
+from redpanda_amd.scan import make_scan_args
+
+
+def _dev(t):
+    return None if t is None else t.to("cuda").contiguous()
+
+
+def scan_fwd(c, bidirectional=False, with_ckpt=False, with_state=False):
+    lib = _lib.load()
+    delta, u, Bc, Cc = (_dev(c[k]) for k in ("delta", "u", "Bc", "Cc"))
+    Ar, Ai, Tk = (_dev(None if c[k] is None else c[k].float()) for k in ("Ar", "Ai", "Tk"))
+    B, L, D = u.shape
+    N = Bc.shape[-1]
+    a = make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional)
+    y = torch.empty((B, L, D), dtype=torch.float32, device="cuda")
+    ckpt = None
+    if with_ckpt:
+        nb = lib.rp_scan_ckpt_bytes(ctypes.byref(a))
+        assert nb >= 0
+        ckpt = torch.empty(max(nb // 4, 1), dtype=torch.float32, device="cuda")
+    h = b = None
+    if with_state:
+        h = torch.empty((B, D, N), dtype=torch.float32, device="cuda")
+        b = torch.empty((B, D, N), dtype=torch.float32, device="cuda")
+    out = _lib.ScanFwdOut(y.data_ptr(), _lib.ptr(ckpt), _lib.ptr(h), _lib.ptr(b))
+    _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out), _lib.stream_of("cuda")), lib)
+    keep = (delta, u, Bc, Cc, Ar, Ai, Tk)
+    return y, ckpt, (h, b), (a, keep)
+
+
+def scan_fwd_bwd(c, bidirectional=False, dh_last=None, dbeta_last=None):
+    """Forward with checkpoints, then backward with upstream c['dy'] -> fp32 grads."""
+    lib = _lib.load()
+    y, ckpt, _, (a, keep) = scan_fwd(c, bidirectional, with_ckpt=True)
+    delta, u, Bc, Cc, Ar, Ai, Tk = keep
+    B, L, D = u.shape
+    N = Bc.shape[-1]
+    f32 = dict(dtype=torch.float32, device="cuda")
+    dy = _dev(c["dy"].float())
+    g = {"delta": torch.empty((B, L, D), **f32), "u": torch.empty((B, L, D), **f32),
+         "Bc": torch.empty((B, L, N), **f32), "Cc": torch.empty((B, L, N), **f32),
+         "Ar": None if Ar is None else torch.empty_like(Ar),
+         "Ai": None if Ai is None else torch.empty_like(Ai),
+         "Tk": None if Tk is None else torch.empty_like(Tk)}
+    wb = lib.rp_scan_bwd_work_bytes(ctypes.byref(a))
+    work = torch.empty(max(wb, 256), dtype=torch.uint8, device="cuda")
+    dh = _dev(dh_last)
+    db = _dev(dbeta_last)
+    io = _lib.ScanBwdIO(dy=dy.data_ptr(), ckpt=_lib.ptr(ckpt), dh_last=_lib.ptr(dh),
+                        dbeta_last=_lib.ptr(db), d_delta=g["delta"].data_ptr(),
+                        d_u=g["u"].data_ptr(), d_Bc=g["Bc"].data_ptr(), d_Cc=g["Cc"].data_ptr(),
+                        d_A_real=_lib.ptr(g["Ar"]), d_A_imag=_lib.ptr(g["Ai"]),
+                        d_track=_lib.ptr(g["Tk"]), work=work.data_ptr(), work_bytes=work.numel())
+    _lib.check(lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), _lib.stream_of("cuda")), lib)
+    torch.cuda.synchronize()
+    return y.cpu(), {k: (None if v is None else v.cpu()) for k, v in g.items()}

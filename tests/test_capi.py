@@ -1,0 +1,141 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and its host-side validation rejects bad arguments with a
+negative status and a message (no kernel is launched on these paths)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from redpanda_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                      "include", "redpanda_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rp_[a-z_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.open_library()
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version(lib):
+    assert lib.rp_abi_version() == _lib.ABI_VERSION
+
+
+def _good_args(**kw):
+    a = _lib.ScanArgs()
+    a.B, a.L, a.D, a.N, a.NR, a.NT = 2, 64, 128, 40, 32, 8
+    a.dtype_delta = a.dtype_u = a.dtype_B = a.dtype_C = _lib.RP_BF16
+    fake = 0x10000  # never dereferenced: validation only
+    a.delta = a.u = a.Bc = a.Cc = fake
+    a.delta_sb, a.delta_sl = 64 * 128, 128
+    a.u_sb, a.u_sl = 64 * 128, 128
+    a.Bc_sb, a.Bc_sl = 64 * 40, 40
+    a.Cc_sb, a.Cc_sl = 64 * 40, 40
+    a.A_real = a.A_imag = a.track = fake
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_valid_args_pass_check(lib):
+    assert lib.rp_scan_check(ctypes.byref(_good_args())) == 0
+
+
+@pytest.mark.parametrize("field,value,needle", [
+    ("N", 41, "NR+NT"),
+    ("NR", -1, "negative"),
+    ("N", 0, "outside"),
+    ("dtype_u", 7, "dtype"),
+    ("bidirectional", 2, "bidirectional"),
+    ("delta", None, "NULL"),
+    ("track", None, "track"),
+    ("u_sl", -5, "stride"),
+    ("reserved", 1, "reserved"),
+])
+def test_invalid_scan_args_rejected(lib, field, value, needle):
+    kw = {field: value}
+    if field == "N" and value == 0:
+        kw.update(NR=0, NT=0)
+    a = _good_args(**kw)
+    st = lib.rp_scan_check(ctypes.byref(a))
+    assert st < 0
+    assert needle in lib.rp_last_error().decode()
+
+
+def test_state_too_large_is_unsupported(lib):
+    a = _good_args(N=200, NR=192, NT=8)
+    assert lib.rp_scan_check(ctypes.byref(a)) == -2
+
+
+def test_workspace_queries(lib):
+    a = _good_args()
+    ck = lib.rp_scan_ckpt_bytes(ctypes.byref(a))
+    wk = lib.rp_scan_bwd_work_bytes(ctypes.byref(a))
+    assert ck > 0 and wk > 0 and wk % 256 == 0
+    a1 = _good_args(L=8)  # a single checkpoint chunk needs no stored checkpoint
+    assert lib.rp_scan_ckpt_bytes(ctypes.byref(a1)) == 0
+    bad = _good_args(N=3)
+    assert lib.rp_scan_ckpt_bytes(ctypes.byref(bad)) == -1
+
+
+def test_final_state_rejected_for_bidirectional(lib):
+    a = _good_args(bidirectional=1)
+    out = _lib.ScanFwdOut(0x10000, None, 0x10000, 0x10000)
+    assert lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out), None) < 0
+    assert "causal" in lib.rp_last_error().decode()
+
+
+def test_bwd_workspace_too_small_rejected(lib):
+    a = _good_args()
+    f = 0x10000
+    io = _lib.ScanBwdIO(dy=f, ckpt=f, d_delta=f, d_u=f, d_Bc=f, d_Cc=f, d_A_real=f,
+                        d_A_imag=f, d_track=f, work=f, work_bytes=16)
+    assert lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), None) == -4
+
+
+def _step_args(**kw):
+    a = _lib.StepArgs()
+    a.R, a.D, a.N, a.NR, a.NT = 16, 64, 20, 16, 4
+    f = 0x10000
+    a.delta = a.u = a.Bc = a.Cc = a.A_real = a.A_imag = a.track = a.Dskip = f
+    a.h_in = a.beta_in = a.h_out = a.beta_out = a.y = f
+    a.delta_sr = a.u_sr = 64
+    a.Bc_sr = a.Cc_sr = 20
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_step_check(lib):
+    assert lib.rp_step_check(ctypes.byref(_step_args())) == 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(beta_in=None))) < 0
+    assert "together" in lib.rp_last_error().decode()
+    assert lib.rp_step_check(ctypes.byref(_step_args(Bc_sr=3))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(NT=5))) < 0
+
+
+def test_initial_state_rules(lib):
+    f = 0x10000
+    assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f))) == 0
+    assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f))) < 0
+    assert "together" in lib.rp_last_error().decode()
+    assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f, bidirectional=1))) < 0
+    assert "causal" in lib.rp_last_error().decode()
+    assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f, L=0))) < 0

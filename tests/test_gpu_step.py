@@ -1,0 +1,178 @@
+"""GPU parity of the fused step kernel: against the reference's step
+(golden fixture and oracle), step == scan (bit-exact, same arithmetic),
+batched == singles, and K-step chains (engine/mars_diagnostics.py:94-164)."""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import scan_ref
+from tests.conftest import load_golden
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+
+
+def _step():
+    from redpanda_amd.step import hip_step
+    return hip_step
+
+
+def rel(a, b):
+    return scan_ref.rel_err(a.detach().cpu(), b.detach().cpu())
+
+
+def make_step_case(seed, R, D, NR, NT, complex_=True):
+    gen = torch.Generator().manual_seed(seed)
+    N = NR + NT
+    dt = F.softplus(torch.randn(R, D, generator=gen) * 0.5 - 2.0)
+    u = torch.randn(R, D, generator=gen)
+    Bc = torch.randn(R, N, generator=gen)
+    Cc = torch.randn(R, N, generator=gen)
+    Ar = -torch.exp(torch.rand(D, NR, generator=gen) * 3.0) if NR else None
+    Ai = (torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi if (NR and complex_) else None
+    Tk = torch.tanh(torch.randn(D, NT, generator=gen) * 1.5) if NT else None
+    Dk = torch.randn(D, generator=gen)
+    h = torch.randn(R, D, N, generator=gen)
+    b = torch.randn(R, D, N, generator=gen) * 0.3
+    return dict(delta=dt, u=u, Bc=Bc, Cc=Cc, Ar=Ar, Ai=Ai, Tk=Tk, D=Dk, h=h, beta=b)
+
+
+def to(t):
+    return None if t is None else t.to(dev)
+
+
+@pytest.mark.parametrize("NR,NT,cplx", [(16, 4, True), (12, 4, True), (8, 0, False), (0, 5, True),
+                                        (32, 8, True), (64, 8, True)])
+@pytest.mark.parametrize("fresh", [False, True])
+def test_step_matches_reference_step(gpu_lib, NR, NT, cplx, fresh):
+    hip_step = _step()
+    c = make_step_case(10 + NR + NT, R=5, D=70, NR=NR, NT=NT, complex_=cplx)
+    state = None if fresh else (c["h"], c["beta"])
+    y_ref, (h_ref, b_ref) = scan_ref.step_core_ref(c["delta"], c["u"], c["Bc"], c["Cc"], c["Ar"],
+                                                   c["Ai"], c["Tk"], c["D"], state)
+    st = None if fresh else (to(c["h"]), to(c["beta"]))
+    y, (h, b) = hip_step(to(c["delta"]), to(c["u"]), to(c["Bc"]), to(c["Cc"]), to(c["Ar"]),
+                         to(c["Ai"]), to(c["Tk"]), to(c["D"]), st)
+    eh, eb, ey = rel(h, h_ref), rel(b, b_ref), rel(y, y_ref)
+    print(f"NR={NR} NT={NT} fresh={fresh}: h {eh:.1e} beta {eb:.1e} y {ey:.1e}")
+    assert eh <= 1e-6 and ey <= 1e-6
+    assert torch.equal(b.cpu(), b_ref), "beta = (dt*u)*B is computed exactly as the reference"
+
+
+def test_step_matches_golden_block_step(gpu_lib):
+    """The SSM core of the reference's Mamba3Block.step on its own fixture."""
+    g = load_golden("step_rot_trk")
+    from oracle import model_ref
+    cfg = model_ref.MambaConfig(vocab_size=64, n_layer=1, d_model=8, d_state=12,
+                                n_track_state=4, mimo_p=2)
+    blk = model_ref.Mamba3Block(cfg).eval()
+    blk.load_state_dict({k[3:]: v for k, v in g.items() if k.startswith("sd.")})
+    hip_step = _step()
+    with torch.no_grad():
+        xb, z = blk.in_proj(g["x"]).chunk(2, dim=-1)
+        xb = F.silu(xb)
+        delta, Bm, Cm = blk._ssm_proj(xb)
+        Ar, Ai = blk._compute_A()
+        y, (h, b) = hip_step(to(delta), to(xb), to(Bm.sum(-1)), to(Cm.sum(-1)), to(Ar), to(Ai),
+                             to(blk._track_gate()), to(blk.D), (to(g["h0"]), to(g["beta0"])))
+        out = blk.out_proj(y.cpu() * F.silu(z))
+    assert rel(h, g["h"]) <= 1e-6
+    assert rel(b, g["beta"]) <= 1e-6
+    assert rel(out, g["out"]) <= 1e-5
+
+
+@pytest.mark.parametrize("NR,NT,L", [(12, 4, 37), (32, 8, 64), (16, 4, 20), (64, 8, 19)])
+def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
+    """Stepping token by token reproduces the scan's y and final state bit for bit."""
+    from redpanda_amd.scan import hip_scan_with_state
+    hip_step = _step()
+    gen = torch.Generator().manual_seed(NR * 100 + L)
+    B, D = 3, 72
+    N = NR + NT
+    dt = F.softplus(torch.randn(B, L, D, generator=gen) * 0.5 - 2.0).to(dev)
+    u = torch.randn(B, L, D, generator=gen).to(dev)
+    Bc = torch.randn(B, L, N, generator=gen).to(dev)
+    Cc = torch.randn(B, L, N, generator=gen).to(dev)
+    Ar = (-torch.exp(torch.rand(D, NR, generator=gen) * 3.0)).to(dev)
+    Ai = ((torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi).to(dev)
+    Tk = torch.tanh(torch.randn(D, NT, generator=gen) * 1.5).to(dev)
+    Dz = torch.zeros(D, device=dev)
+    with torch.no_grad():
+        y_scan, (h_scan, b_scan) = hip_scan_with_state(dt, u, Bc, Cc, Ar, Ai, Tk)
+        state, ys = None, []
+        for t in range(L):
+            yt, state = hip_step(dt[:, t], u[:, t], Bc[:, t], Cc[:, t], Ar, Ai, Tk, Dz, state)
+            ys.append(yt)
+    assert torch.equal(torch.stack(ys, 1), y_scan)
+    assert torch.equal(state[0], h_scan)
+    assert torch.equal(state[1], b_scan)
+
+
+def test_scan_prefix_then_step_continues(gpu_lib):
+    """scan([0, s)) state + steps over [s, L) == scan([0, L)) (bitwise)."""
+    from redpanda_amd.scan import hip_scan_with_state
+    hip_step = _step()
+    gen = torch.Generator().manual_seed(77)
+    B, L, D, NR, NT, s = 2, 30, 64, 16, 4, 11
+    N = NR + NT
+    dt = F.softplus(torch.randn(B, L, D, generator=gen) * 0.5 - 2.0).to(dev)
+    u = torch.randn(B, L, D, generator=gen).to(dev)
+    Bc = torch.randn(B, L, N, generator=gen).to(dev)
+    Cc = torch.randn(B, L, N, generator=gen).to(dev)
+    Ar = (-torch.exp(torch.rand(D, NR, generator=gen) * 3.0)).to(dev)
+    Ai = ((torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi).to(dev)
+    Tk = torch.tanh(torch.randn(D, NT, generator=gen)).to(dev)
+    Dz = torch.zeros(D, device=dev)
+    with torch.no_grad():
+        y_full, _ = hip_scan_with_state(dt, u, Bc, Cc, Ar, Ai, Tk)
+        _, state = hip_scan_with_state(dt[:, :s].contiguous(), u[:, :s].contiguous(),
+                                       Bc[:, :s].contiguous(), Cc[:, :s].contiguous(), Ar, Ai, Tk)
+        for t in range(s, L):
+            yt, state = hip_step(dt[:, t], u[:, t], Bc[:, t], Cc[:, t], Ar, Ai, Tk, Dz, state)
+            assert torch.equal(yt, y_full[:, t]), t
+
+
+def test_batched_equals_singles_and_chains(gpu_lib):
+    """(a) one batched step == N single steps; (b) a K-step batched chain == K
+    single chains (engine/mars_diagnostics.py:110-143)."""
+    hip_step = _step()
+    c = make_step_case(42, R=6, D=96, NR=16, NT=4)
+    p = [to(c[k]) for k in ("Ar", "Ai", "Tk", "D")]
+    gen = torch.Generator().manual_seed(3)
+    K = 8
+    dts = F.softplus(torch.randn(K, 6, 96, generator=gen) * 0.5 - 2).to(dev)
+    us = torch.randn(K, 6, 96, generator=gen).to(dev)
+    Bs = torch.randn(K, 6, 20, generator=gen).to(dev)
+    Cs = torch.randn(K, 6, 20, generator=gen).to(dev)
+    st = (to(c["h"]), to(c["beta"]))
+    with torch.no_grad():
+        yb, _ = hip_step(dts[0], us[0], Bs[0], Cs[0], *p, st)
+        for i in range(6):
+            yi, _ = hip_step(dts[0, i:i + 1], us[0, i:i + 1], Bs[0, i:i + 1], Cs[0, i:i + 1], *p,
+                             (st[0][i:i + 1].clone(), st[1][i:i + 1].clone()))
+            assert torch.equal(yi[0], yb[i])
+        chain = st
+        for k in range(K):
+            yk, chain = hip_step(dts[k], us[k], Bs[k], Cs[k], *p, chain)
+        for i in range(6):
+            si = (st[0][i:i + 1].clone(), st[1][i:i + 1].clone())
+            for k in range(K):
+                yi, si = hip_step(dts[k, i:i + 1], us[k, i:i + 1], Bs[k, i:i + 1],
+                                  Cs[k, i:i + 1], *p, si)
+            assert torch.equal(yi[0], yk[i])
+            assert torch.equal(si[0][0], chain[0][i])
+
+
+def test_in_place_state_update(gpu_lib):
+    hip_step = _step()
+    c = make_step_case(43, R=4, D=64, NR=16, NT=4)
+    p = [to(c[k]) for k in ("delta", "u", "Bc", "Cc", "Ar", "Ai", "Tk", "D")]
+    h, b = to(c["h"]), to(c["beta"])
+    with torch.no_grad():
+        y1, (h1, b1) = hip_step(*p, (h.clone(), b.clone()))
+        y2 = torch.empty_like(y1)
+        hip_step(*p, (h, b), out=(y2, h, b))
+    assert torch.equal(y1, y2) and torch.equal(h1, h) and torch.equal(b1, b)
