@@ -1,0 +1,387 @@
+"""Throughput of the hot path on one MI355X: the trapezoidal selective scan
+(bidirectional forward + analytic backward at the Eval-Mamba training shape)
+and the batched O(1) step (4096 rollouts x 8 layers).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step]
+
+One "step" of the headline workload is one forward + backward of one
+bidirectional scan layer over a batch of 256 boards x 64 tokens, d_inner 1536
+(24 heads x 64), d_state 40 (32 rotational + 8 tanh-tracking), bf16-stored
+inputs, fp32 arithmetic and fp32 gradients, through the product's autograd
+entry (redpanda_amd.scan.hip_trapezoidal_scan).  Inputs are synthetic and
+resident in HBM before the timed region.  Tokens are counted once per
+forward + backward (both directions fused).
+
+Besides the headline number the JSON line carries:
+  roofline      the dominant kernel's algorithmic bytes / measured duration
+                (HIP events on the launch stream) against 8 TB/s;
+  kernels       the same for every kernel of the path;
+  step          rollout-steps/s of the fused step kernel over 8 layers;
+  cpu_baseline  the reference's CPU PyTorch path (the oracle's fp32
+                restatement) on a bounded sample, on this host's cores.
+Only one GPU is used; --gpus above 1 exits with a message.
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+
+# Eval-Mamba training shape of one layer: batch 256, L=64 board tokens,
+# d_model 768, expand 2 -> d_inner 1536 (24 heads x 64), d_state 32 complex
+# plus 8 tanh-tracking channels.
+SCAN_SHAPE = dict(B=256, L=64, D=1536, NR=32, NT=8)
+# Search-Mamba batched step: 4096 rollouts, 8 causal layers, d_model 512
+# (d_inner 1024 = 16 heads x 64), d_state 16 complex plus 4 tracking.
+STEP_SHAPE = dict(R=4096, layers=8, D=1024, NR=16, NT=4)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-step", action="store_true", help="skip the step() workload")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="approximate budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+def scan_inputs(B, L, D, NR, NT, seed, device, dtype):
+    """dt = softplus(N(-2, .5)); x, B, C ~ N(0, 1) with B/C RMS-normalised per
+    token; Ar = -exp(U(0, 3)); Ai = U(-pi, pi); Tk = tanh(N(0, 1.5));
+    dout ~ N(0, 1).  Generated on the CPU in fp32, stored in `dtype`."""
+    import torch
+    import torch.nn.functional as F
+    gen = torch.Generator().manual_seed(seed)
+    N = NR + NT
+    u = torch.randn(B, L, D, generator=gen)
+    dt = F.softplus(torch.randn(B, L, D, generator=gen) * 0.5 - 2.0)
+    Bc = torch.randn(B, L, N, generator=gen)
+    Cc = torch.randn(B, L, N, generator=gen)
+    Bc = Bc / Bc.pow(2).mean(-1, keepdim=True).sqrt()
+    Cc = Cc / Cc.pow(2).mean(-1, keepdim=True).sqrt()
+    Ar = -torch.exp(torch.rand(D, NR, generator=gen) * 3.0)
+    Ai = (torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi
+    Tk = torch.tanh(torch.randn(D, NT, generator=gen) * 1.5)
+    dy = torch.randn(B, L, D, generator=gen)
+    st = [t.to(dtype).to(device) for t in (dt, u, Bc, Cc)]
+    return dict(delta=st[0], u=st[1], Bc=st[2], Cc=st[3], Ar=Ar.to(device), Ai=Ai.to(device),
+                Tk=Tk.to(device), dy=dy.to(device), N=N, NR=NR)
+
+
+def scan_bytes(B, L, D, N, NR, NT, s_in, bidirectional):
+    """Algorithmic HBM bytes of one forward and one backward launch.
+
+    forward : read delta, u (s_in each per channel) and B, C (s_in per state),
+              write y (fp32): T*(D*(2 s_in + 4) + 2 N s_in); parameters
+              Ar, Ai (D x NR) and Tk (D x NT) in fp32.  Both directions of a
+              bidirectional layer share one read of the inputs.
+    backward: read delta, u, B, C (s_in) and dy (fp32), write d_delta, d_u,
+              d_B, d_C (fp32): T*(D*(2 s_in + 4 + 8) + N*(2 s_in + 8));
+              parameters read once and their gradients written once.
+    """
+    T = B * L
+    par = (2 * D * NR + D * NT) * 4
+    fwd = T * (D * (2 * s_in + 4) + 2 * N * s_in) + par
+    bwd = T * (D * (2 * s_in + 12) + N * (2 * s_in + 8)) + 2 * par
+    return fwd, bwd
+
+
+def step_bytes(R, D, N, NR, NT):
+    """Algorithmic HBM bytes of one fused step launch: read and write h and
+    beta (fp32, 16 B per state element), read delta and u, write y (12 B per
+    channel), read B and C (8 B per state), per rollout; plus parameters."""
+    return R * (16 * D * N + 12 * D + 8 * N) + (2 * D * NR + D * NT + D) * 4
+
+
+class EventTimer:
+    """Average GPU duration of a launch sequence, with events on the stream
+    the kernels are launched on (torch's current stream)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def time(self, fn, reps):
+        torch = self.torch
+        s = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            fn()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3  # seconds per call
+
+
+def bench_scan(torch, args, dtype):
+    from redpanda_amd import _lib
+    from redpanda_amd.scan import hip_trapezoidal_scan, make_scan_args
+    sh = SCAN_SHAPE
+    B, L, D, NR, NT = sh["B"], sh["L"], sh["D"], sh["NR"], sh["NT"]
+    N = NR + NT
+    dev = torch.device("cuda:0")
+    c = scan_inputs(B, L, D, NR, NT, 1003, dev, dtype)
+    leaves = [c[k].requires_grad_(True) for k in ("delta", "u", "Bc", "Cc", "Ar", "Ai", "Tk")]
+    dy = c["dy"]
+
+    def one_step():
+        for t in leaves:
+            t.grad = None
+        y = hip_trapezoidal_scan(*leaves[:4], leaves[4], leaves[5], leaves[6], NR, N,
+                                 bidirectional=True)
+        y.backward(dy)
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    tok_s = B * L * args.steps / elapsed
+
+    # per-kernel durations through the C ABI with preallocated buffers
+    lib = _lib.load()
+    f32 = dict(dtype=torch.float32, device=dev)
+    a = make_scan_args(c["delta"], c["u"], c["Bc"], c["Cc"], c["Ar"].detach(), c["Ai"].detach(),
+                       c["Tk"].detach(), True)
+    y = torch.empty((B, L, D), **f32)
+    nck = lib.rp_scan_ckpt_bytes(ctypes.byref(a))
+    ckpt = torch.empty(max(nck // 4, 1), **f32)
+    out_ck = _lib.ScanFwdOut(y.data_ptr(), ckpt.data_ptr(), None, None)
+    out_inf = _lib.ScanFwdOut(y.data_ptr(), None, None, None)
+    g = [torch.empty((B, L, D), **f32), torch.empty((B, L, D), **f32),
+         torch.empty((B, L, N), **f32), torch.empty((B, L, N), **f32),
+         torch.empty((D, NR), **f32), torch.empty((D, NR), **f32), torch.empty((D, NT), **f32)]
+    wb = lib.rp_scan_bwd_work_bytes(ctypes.byref(a))
+    work = torch.empty(max(wb, 256), dtype=torch.uint8, device=dev)
+    io = _lib.ScanBwdIO(dy=dy.data_ptr(), ckpt=ckpt.data_ptr(), d_delta=g[0].data_ptr(),
+                        d_u=g[1].data_ptr(), d_Bc=g[2].data_ptr(), d_Cc=g[3].data_ptr(),
+                        d_A_real=g[4].data_ptr(), d_A_imag=g[5].data_ptr(),
+                        d_track=g[6].data_ptr(), work=work.data_ptr(), work_bytes=work.numel())
+    stream = _lib.stream_of(dev)
+
+    def fwd_train():
+        _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out_ck), stream), lib)
+
+    def fwd_inf():
+        _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out_inf), stream), lib)
+
+    def bwd():
+        _lib.check(lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), stream), lib)
+
+    timer = EventTimer(torch)
+    reps = max(args.steps, 5)
+    fwd_train()
+    bwd()
+    t_fwd = timer.time(fwd_train, reps)
+    t_inf = timer.time(fwd_inf, reps)
+    t_bwd = timer.time(bwd, reps)   # includes the two small reduction kernels
+    s_in = 2 if dtype != torch.float32 else 4
+    fb, bb = scan_bytes(B, L, D, N, NR, NT, s_in, True)
+    kern = [
+        {"kernel": "scan_fwd_kernel (bidirectional, checkpoints)", "seconds": t_fwd,
+         "alg_bytes": fb, "GBps": fb / t_fwd / 1e9},
+        {"kernel": "scan_fwd_kernel (bidirectional, inference)", "seconds": t_inf,
+         "alg_bytes": fb, "GBps": fb / t_inf / 1e9},
+        {"kernel": "scan_bwd_kernel + reductions", "seconds": t_bwd,
+         "alg_bytes": bb, "GBps": bb / t_bwd / 1e9},
+    ]
+    return dict(tok_s=tok_s, elapsed=elapsed, kernels=kern, t_fwd=t_fwd, t_bwd=t_bwd,
+                t_inf=t_inf, fwd_bytes=fb, bwd_bytes=bb, T=B * L)
+
+
+def bench_step(torch, args):
+    from redpanda_amd import _lib
+    sh = STEP_SHAPE
+    R, layers, D, NR, NT = sh["R"], sh["layers"], sh["D"], sh["NR"], sh["NT"]
+    N = NR + NT
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(1004)
+    import torch.nn.functional as F
+    lib = _lib.load()
+    f32 = dict(dtype=torch.float32, device=dev)
+    per_layer = []
+    for _ in range(layers):
+        dt = F.softplus(torch.randn(R, D, generator=gen) * 0.5 - 2.0).to(dev)
+        u = torch.randn(R, D, generator=gen).to(dev)
+        Bc = torch.randn(R, N, generator=gen)
+        Cc = torch.randn(R, N, generator=gen)
+        Bc = (Bc / Bc.pow(2).mean(-1, keepdim=True).sqrt()).to(dev)
+        Cc = (Cc / Cc.pow(2).mean(-1, keepdim=True).sqrt()).to(dev)
+        Ar = (-torch.exp(torch.rand(D, NR, generator=gen) * 3.0)).to(dev)
+        Ai = ((torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi).to(dev)
+        Tk = torch.tanh(torch.randn(D, NT, generator=gen) * 1.5).to(dev)
+        Dk = torch.randn(D, generator=gen).to(dev)
+        h = torch.zeros((R, D, N), **f32)
+        beta = torch.zeros((R, D, N), **f32)
+        y = torch.empty((R, D), **f32)
+        a = _lib.StepArgs()
+        a.R, a.D, a.N, a.NR, a.NT = R, D, N, NR, NT
+        a.delta, a.delta_sr = dt.data_ptr(), D
+        a.u, a.u_sr = u.data_ptr(), D
+        a.Bc, a.Bc_sr = Bc.data_ptr(), N
+        a.Cc, a.Cc_sr = Cc.data_ptr(), N
+        a.h_in, a.beta_in = h.data_ptr(), beta.data_ptr()
+        a.A_real, a.A_imag, a.track = Ar.data_ptr(), Ai.data_ptr(), Tk.data_ptr()
+        a.Dskip = Dk.data_ptr()
+        a.h_out, a.beta_out, a.y = h.data_ptr(), beta.data_ptr(), y.data_ptr()  # in place
+        per_layer.append((a, (dt, u, Bc, Cc, Ar, Ai, Tk, Dk, h, beta, y)))
+    stream = _lib.stream_of(dev)
+
+    def ply():
+        for a, _ in per_layer:
+            _lib.check(lib.rp_step(ctypes.byref(a), stream), lib)
+
+    for _ in range(max(args.warmup, 1)):
+        ply()
+    torch.cuda.synchronize()
+    plies = 32
+    t0 = time.perf_counter()
+    for _ in range(plies):
+        ply()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer = EventTimer(torch)
+    t_launch = timer.time(ply, plies) / layers
+    nb = step_bytes(R, D, N, NR, NT)
+    return dict(rollout_steps_s=R * plies / elapsed, plies=plies, elapsed=elapsed,
+                t_launch=t_launch, bytes=nb, GBps=nb / t_launch / 1e9)
+
+
+def cpu_baseline(budget_s):
+    """The reference's CPU PyTorch path: the fp32 chunk-streaming Hillis-Steele
+    scan with per-chunk checkpointing (engine/mamba.py:318-423), both
+    directions, forward + autograd backward, on a reduced batch of the same
+    Eval-Mamba layer shape (bf16-rounded inputs upcast to fp32)."""
+    import torch
+    from oracle import scan_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    sh = SCAN_SHAPE
+    Bs = 8
+    c = scan_inputs(Bs, sh["L"], sh["D"], sh["NR"], sh["NT"], 1003, "cpu", torch.bfloat16)
+    args = [c[k].float() if c[k].dtype != torch.float32 else c[k]
+            for k in ("delta", "u", "Bc", "Cc", "Ar", "Ai", "Tk")]
+    N = c["N"]
+
+    def run():
+        lv = [t.clone().requires_grad_(True) for t in args]
+        yf, _ = scan_ref.contracted_scan_ref(*lv, N, checkpoint=True)
+        yr, _ = scan_ref.contracted_scan_ref(lv[0].flip(1), lv[1].flip(1), lv[2].flip(1),
+                                             lv[3].flip(1), lv[4], lv[5], lv[6], N,
+                                             checkpoint=True)
+        ((yf + yr.flip(1)) * c["dy"]).sum().backward()
+
+    for _ in range(2):
+        run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * budget_s:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": Bs * sh["L"] / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"oracle fp32 restatement of the reference CPU scan (chunk-streaming "
+                       f"Hillis-Steele, per-chunk checkpoint), bidirectional fwd+bwd, "
+                       f"B={Bs} L={sh['L']} D={sh['D']} N={N}; median of {len(times)} runs"),
+            "cpu_model": cpu_model, "os_cpu_count": os.cpu_count(),
+            "torch": torch.__version__}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); "
+              "the scan and step shard by batch / rollout with no exchange, so N GPUs "
+              "run N independent copies of this workload.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm GPU visible", file=sys.stderr)
+        sys.exit(1)
+    print(f"[bench] scan fwd+bwd {SCAN_SHAPE} bf16 storage, steps={args.steps} "
+          f"warmup={args.warmup}", file=sys.stderr, flush=True)
+    sc = bench_scan(torch, args, torch.bfloat16)
+    print(f"[bench] scan: {sc['tok_s']:.4g} tokens/s; fwd {sc['t_fwd'] * 1e3:.3f} ms, "
+          f"bwd {sc['t_bwd'] * 1e3:.3f} ms", file=sys.stderr, flush=True)
+    step = None
+    if not args.no_step:
+        print(f"[bench] step {STEP_SHAPE}", file=sys.stderr, flush=True)
+        step = bench_step(torch, args)
+        print(f"[bench] step: {step['rollout_steps_s']:.4g} rollout-steps/s, "
+              f"{step['t_launch'] * 1e6:.1f} us/launch, {step['GBps']:.0f} GB/s",
+              file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] cpu baseline", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(args.cpu_seconds)
+        print(f"[bench] cpu: {cpu['value']:.4g} tokens/s on {cpu['cores']} threads",
+              file=sys.stderr, flush=True)
+
+    # dominant kernel: the longer of forward (training) and backward
+    k_f, k_b = sc["kernels"][0], sc["kernels"][2]
+    dom = k_b if k_b["seconds"] >= k_f["seconds"] else k_f
+    roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"],
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["GBps"] / HBM_PEAK_GBS,
+            "traffic": None, "alg_bytes_per_launch": dom["alg_bytes"],
+            "avg_launch_s": dom["seconds"]}
+    ms = sc["elapsed"] / args.steps * 1e3
+    line = {
+        "metric": "scan fwd+bwd tokens/s & %HBM peak; batched step() rollout-steps/s",
+        "value": sc["tok_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32 (bf16-stored inputs)", "data": "synthetic",
+        "config": {"workload": "Eval-Mamba bidirectional trapezoidal scan layer, fwd+bwd",
+                   "B": SCAN_SHAPE["B"], "L": SCAN_SHAPE["L"], "d_inner": SCAN_SHAPE["D"],
+                   "d_state": SCAN_SHAPE["NR"] + SCAN_SHAPE["NT"], "n_rot": SCAN_SHAPE["NR"],
+                   "n_track": SCAN_SHAPE["NT"], "input_storage": "bf16",
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "kernels": sc["kernels"],
+        "fwd_only_tokens_s": sc["T"] / sc["t_inf"],
+    }
+    if step is not None:
+        line["step"] = {
+            "metric": "rollout-steps/s", "value": step["rollout_steps_s"],
+            "config": {"workload": "Search-Mamba batched step, SSM core over all layers",
+                       **STEP_SHAPE, "d_state": STEP_SHAPE["NR"] + STEP_SHAPE["NT"]},
+            "roofline": {"bound": "hbm", "kernel": "step_kernel",
+                         "achieved": step["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": step["GBps"] / HBM_PEAK_GBS, "traffic": None,
+                         "alg_bytes_per_launch": step["bytes"],
+                         "avg_launch_s": step["t_launch"]},
+        }
+    line["cpu_baseline"] = cpu
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -125,12 +125,13 @@ def selective_scan_ref(u, delta, A_real, A_imag, B, C, D, track, n_state,
     return y
 
 
-def contracted_scan_ref(delta, u, Bc, Cc, A_real, A_imag, track, n_state):
+def contracted_scan_ref(delta, u, Bc, Cc, A_real, A_imag, track, n_state, checkpoint=False):
     """The chunk loop alone on contracted B/C, WITHOUT the D-skip.
 
     This is exactly what the reference's kernel entry replaces
     (engine/triton_scan.py:318-337 is documented as a drop-in for the chunk
-    loop of engine/mamba.py:360-373).
+    loop of engine/mamba.py:360-373).  `checkpoint` recomputes each chunk in
+    backward as scan_checkpoint=True does in training (:358-370).
     """
     batch, L, d_inner = u.shape
     h = torch.zeros((batch, d_inner, n_state), dtype=torch.float32, device=u.device)
@@ -138,9 +139,13 @@ def contracted_scan_ref(delta, u, Bc, Cc, A_real, A_imag, track, n_state):
     outs = []
     for s in range(0, L, SCAN_CHUNK):
         e = min(s + SCAN_CHUNK, L)
-        y_c, h, beta_last = scan_chunk_ref(delta[:, s:e], u[:, s:e], Bc[:, s:e],
-                                           Cc[:, s:e], h, beta_last,
-                                           A_real, A_imag, track)
+        args = (delta[:, s:e], u[:, s:e], Bc[:, s:e], Cc[:, s:e], h, beta_last,
+                A_real, A_imag, track)
+        if checkpoint and torch.is_grad_enabled():
+            y_c, h, beta_last = torch.utils.checkpoint.checkpoint(
+                scan_chunk_ref, *args, use_reentrant=False)
+        else:
+            y_c, h, beta_last = scan_chunk_ref(*args)
         outs.append(y_c)
     return torch.cat(outs, dim=1), (h, beta_last)
 

@@ -91,13 +91,33 @@ def open_library(path=LIB_PATH):
     return lib
 
 
+def hip_runtimes_mapped():
+    """Distinct HIP runtime files mapped into this process (Linux)."""
+    try:
+        with open("/proc/self/maps") as fh:
+            paths = {line.split()[-1] for line in fh if "libamdhip64" in line}
+    except OSError:
+        return set()
+    return {os.path.realpath(p) for p in paths}
+
+
 def load():
-    """The library, for use on a GPU.  Raises if there is no GPU or no library."""
+    """The library, for use on a GPU.  Raises if there is no GPU or no library.
+
+    The library's DT_NEEDED libamdhip64.so.7 must resolve to the runtime torch
+    already loaded (same soname), so torch's streams and allocations are valid
+    handles inside it; a second runtime in the process is an error.
+    """
     global _LIB
     if _LIB is None:
         if not torch.cuda.is_available():
             raise RuntimeError("redpanda_amd: the HIP kernels need a ROCm GPU (none visible)")
-        _LIB = open_library()
+        torch.cuda.init()
+        lib = open_library()
+        rts = hip_runtimes_mapped()
+        if len(rts) > 1:
+            raise RuntimeError(f"redpanda_amd: two HIP runtimes in one process: {sorted(rts)}")
+        _LIB = lib
     return _LIB
 
 

@@ -38,8 +38,9 @@ def _code(t):
         raise TypeError(f"redpanda_amd scan: unsupported dtype {t.dtype}") from None
 
 
-def make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional):
-    """ScanArgs for device tensors (delta/u (B,L,D), Bc/Cc (B,L,N))."""
+def make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional, h0=None, beta0=None):
+    """ScanArgs for device tensors (delta/u (B,L,D), Bc/Cc (B,L,N); optional
+    (B,D,N) fp32 contiguous initial state h0, beta0)."""
     B, L, D = u.shape
     N = Bc.shape[-1]
     NR = 0 if Ar is None else Ar.shape[-1]
@@ -54,6 +55,7 @@ def make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional):
     a.Bc, a.Bc_sb, a.Bc_sl = Bc.data_ptr(), Bc.stride(0), Bc.stride(1)
     a.Cc, a.Cc_sb, a.Cc_sl = Cc.data_ptr(), Cc.stride(0), Cc.stride(1)
     a.A_real, a.A_imag, a.track = _lib.ptr(Ar), _lib.ptr(Ai), _lib.ptr(Tk)
+    a.h0, a.beta0 = _lib.ptr(h0), _lib.ptr(beta0)
     return a
 
 
@@ -82,19 +84,21 @@ def _check_shapes(delta, u, Bc, Cc, Ar, Ai, Tk):
 
 
 class _HipScan(torch.autograd.Function):
-    """y = S(x) (or S(x) + flip(S(flip(x)))), optionally with the final state."""
+    """y = S(x) (or S(x) + flip(S(flip(x)))), optionally from an initial state
+    (h0, beta0) and optionally returning the final state (h_last, beta_last)."""
 
     @staticmethod
-    def forward(ctx, delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional, with_state):
+    def forward(ctx, delta, u, Bc, Cc, Ar, Ai, Tk, h0, beta0, bidirectional, with_state):
         lib = _lib.load()
         delta, u, Bc, Cc = (_inner_contig(t) for t in (delta, u, Bc, Cc))
         Arc, Aic, Tkc = _param(Ar), _param(Ai), _param(Tk)
+        h0c, b0c = _param(h0), _param(beta0)
         B, L, D = u.shape
         N = Bc.shape[-1]
         dev = u.device
-        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, bidirectional)
+        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, bidirectional, h0c, b0c)
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
-        need_grad = any(ctx.needs_input_grad[:7])
+        need_grad = any(ctx.needs_input_grad[:9])
         ckpt = None
         if need_grad:
             nbytes = lib.rp_scan_ckpt_bytes(ctypes.byref(args))
@@ -109,9 +113,9 @@ class _HipScan(torch.autograd.Function):
         ctx.bidirectional = bidirectional
         ctx.with_state = with_state
         ctx.in_dtypes = tuple(None if t is None else t.dtype
-                              for t in (delta, u, Bc, Cc, Ar, Ai, Tk))
+                              for t in (delta, u, Bc, Cc, Ar, Ai, Tk, h0, beta0))
         if need_grad:
-            ctx.save_for_backward(delta, u, Bc, Cc, Arc, Aic, Tkc, ckpt)
+            ctx.save_for_backward(delta, u, Bc, Cc, Arc, Aic, Tkc, h0c, b0c, ckpt)
         if with_state:
             return y, h_last, beta_last
         return y
@@ -119,11 +123,11 @@ class _HipScan(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy, dh_last=None, dbeta_last=None):
         lib = _lib.load()
-        delta, u, Bc, Cc, Arc, Aic, Tkc, ckpt = ctx.saved_tensors
+        delta, u, Bc, Cc, Arc, Aic, Tkc, h0c, b0c, ckpt = ctx.saved_tensors
         B, L, D = u.shape
         N = Bc.shape[-1]
         dev = u.device
-        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, ctx.bidirectional)
+        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, ctx.bidirectional, h0c, b0c)
         f32 = dict(dtype=torch.float32, device=dev)
         dy = torch.zeros((B, L, D), **f32) if dy is None else dy.to(torch.float32).contiguous()
         if dh_last is not None:
@@ -137,17 +141,21 @@ class _HipScan(torch.autograd.Function):
         d_Ar = torch.empty_like(Arc) if Arc is not None else None
         d_Ai = torch.empty_like(Aic) if Aic is not None else None
         d_Tk = torch.empty_like(Tkc) if Tkc is not None else None
+        d_h0 = torch.empty((B, D, N), **f32) if h0c is not None else None
+        d_b0 = torch.empty((B, D, N), **f32) if h0c is not None else None
         wbytes = lib.rp_scan_bwd_work_bytes(ctypes.byref(args))
         _lib.check(0 if wbytes >= 0 else -1, lib)
         work = torch.empty(max(wbytes, 256), dtype=torch.uint8, device=dev)
-        io = _lib.ScanBwdIO(dy.data_ptr(), _lib.ptr(ckpt), _lib.ptr(dh_last), _lib.ptr(dbeta_last),
-                            d_delta.data_ptr(), d_u.data_ptr(), d_B.data_ptr(), d_C.data_ptr(),
-                            _lib.ptr(d_Ar), _lib.ptr(d_Ai), _lib.ptr(d_Tk),
-                            work.data_ptr(), work.numel())
+        io = _lib.ScanBwdIO(dy=dy.data_ptr(), ckpt=_lib.ptr(ckpt), dh_last=_lib.ptr(dh_last),
+                            dbeta_last=_lib.ptr(dbeta_last), d_delta=d_delta.data_ptr(),
+                            d_u=d_u.data_ptr(), d_Bc=d_B.data_ptr(), d_Cc=d_C.data_ptr(),
+                            d_A_real=_lib.ptr(d_Ar), d_A_imag=_lib.ptr(d_Ai),
+                            d_track=_lib.ptr(d_Tk), d_h0=_lib.ptr(d_h0), d_beta0=_lib.ptr(d_b0),
+                            work=work.data_ptr(), work_bytes=work.numel())
         _lib.check(lib.rp_scan_bwd(ctypes.byref(args), ctypes.byref(io), _lib.stream_of(dev)), lib)
-        grads = [d_delta, d_u, d_B, d_C, d_Ar, d_Ai, d_Tk]
+        grads = [d_delta, d_u, d_B, d_C, d_Ar, d_Ai, d_Tk, d_h0, d_b0]
         out = []
-        for g, dt, need in zip(grads, ctx.in_dtypes, ctx.needs_input_grad[:7]):
+        for g, dt, need in zip(grads, ctx.in_dtypes, ctx.needs_input_grad[:9]):
             out.append(g.to(dt) if (g is not None and need) else None)
         return (*out, None, None)
 
@@ -171,12 +179,31 @@ def hip_trapezoidal_scan(delta, u, B_contracted, C_contracted, A_real, A_imag, t
     if B_contracted.shape[-1] != n_state:
         raise ValueError(f"scan: B_contracted has {B_contracted.shape[-1]} states, n_state={n_state}")
     return _HipScan.apply(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
-                          bool(bidirectional), False)
+                          None, None, bool(bidirectional), False)
 
 
-def hip_scan_with_state(delta, u, B_contracted, C_contracted, A_real, A_imag, track):
-    """Causal scan returning (y, (h_last, beta_last)); differentiable in all three."""
+def hip_scan_with_state(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
+                        state=None):
+    """Causal scan continuing from `state` = (h0, beta0) (or the zero state)
+    and returning (y, (h_last, beta_last)): the return_state path of the
+    reference (engine/mamba.py:377-379) on the HIP kernel.  Differentiable in
+    every input, the initial state and both outputs.  h_last, beta_last are
+    exactly the cache step() continues from."""
     _check_shapes(delta, u, B_contracted, C_contracted, A_real, A_imag, track)
+    h0 = beta0 = None
+    if state is not None:
+        h0, beta0 = state
+        B, L, D = u.shape
+        N = B_contracted.shape[-1]
+        if h0.shape != (B, D, N) or beta0.shape != (B, D, N):
+            raise ValueError(f"scan: initial state must be (B, D, N) = {(B, D, N)}")
+        if L < 1:
+            raise ValueError("scan: an initial state needs L >= 1")
     y, h, beta = _HipScan.apply(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
-                                False, True)
+                                h0, beta0, False, True)
     return y, (h, beta)
+
+
+# Names the reference's callers import (engine/mamba.py:344).
+HAS_TRITON = HAS_HIP
+triton_trapezoidal_scan = hip_trapezoidal_scan

@@ -139,3 +139,28 @@ def test_initial_state_rules(lib):
     assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f, bidirectional=1))) < 0
     assert "causal" in lib.rp_last_error().decode()
     assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f, L=0))) < 0
+
+
+def _header_struct_fields(name):
+    """Field names of `typedef struct name {...} name;` in declaration order."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (name, name), text, flags=re.S).group(1)
+    fields = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        # "int64_t B, L, D" / "const void* delta" / "float* y"
+        head, *rest = [p.strip() for p in decl.split(",")]
+        fields.append(re.findall(r"[A-Za-z_][A-Za-z0-9_]*", head)[-1])
+        fields.extend(rest)
+    return fields
+
+
+@pytest.mark.parametrize("cname,pyname", [("rp_scan_args", "ScanArgs"),
+                                          ("rp_scan_fwd_out", "ScanFwdOut"),
+                                          ("rp_scan_bwd_io", "ScanBwdIO"),
+                                          ("rp_step_args", "StepArgs")])
+def test_ctypes_structs_mirror_header(cname, pyname):
+    py = [f[0] for f in getattr(_lib, pyname)._fields_]
+    assert py == _header_struct_fields(cname)
