@@ -35,13 +35,14 @@ int64_t elem_size(int dtype) { return dtype == RP_F32 ? 4 : 2; }
 
 int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
 
-// Lanes-per-channel override for tuning (RP_LANES_PER_CHANNEL=4 or 8).
+// Lanes-per-channel override for tuning (RP_LANES_PER_CHANNEL=4, 8 or 16;
+// a size the override cannot hold falls through to the next larger split).
 int lanes_override() {
   static int v = [] {
     const char* s = getenv("RP_LANES_PER_CHANNEL");
     if (s == nullptr) return 0;
     const int x = atoi(s);
-    return (x == 4 || x == 8) ? x : 0;
+    return (x == 4 || x == 8 || x == 16) ? x : 0;
   }();
   return v;
 }
@@ -118,14 +119,14 @@ Plan make_plan(const rp_scan_args* a) {
   pl.ndir = a->bidirectional ? 2 : 1;
   // batch rows per backward workgroup: enough workgroups to fill 256 CUs
   // several times over, while amortising the parameter-gradient partials
-  int64_t bg = (a->B * (int64_t)pl.ntiles) / 2048;
+  int64_t bg = (a->B * (int64_t)pl.ntiles) / 3072;
   if (bg < 1) bg = 1;
   if (bg > 8) bg = 8;
   pl.bg = (int)bg;
   pl.nbg = (int)((a->B + bg - 1) / bg);
   pl.ckpt_bytes = (int64_t)pl.ndir * a->B * pl.nck * pl.ntiles * rp::kThreads * NPL * 4;
   pl.part_bc_bytes = round_up(2 * (int64_t)pl.ntiles * a->B * a->L * a->N * 4, 256);
-  pl.part_par_bytes = round_up((int64_t)pl.nbg * 2 * a->D * a->N * 4, 256);
+  pl.part_par_bytes = round_up((int64_t)pl.nbg * 2 * a->D * a->N * 8, 256);
   return pl;
 }
 
@@ -169,10 +170,14 @@ rp::ScanParams scan_params(const rp_scan_args* a, const Plan& pl) {
 namespace rp {
 
 bool choose_shape(int N, int* S, int* NPL) {
-  static const int npl4[] = {1, 2, 3, 4, 5, 6, 8, 10};
-  static const int npl8[] = {6, 8, 9, 10, 12, 16};
+  // lanes per channel grow with the state size so that a lane holds at most
+  // a handful of states (the backward keeps K steps of three per-state
+  // values in registers); 16-lane rows keep every channel inside one row
+  static const int npl4[] = {1, 2, 3, 4, 5};
+  static const int npl8[] = {3, 4, 5};
+  static const int npl16[] = {3, 4, 5, 6, 8};
   const int force = lanes_override();
-  if (N <= 40 && force != 8) {
+  if ((force == 0 && N <= 20) || force == 4) {
     for (int v : npl4)
       if (4 * v >= N) {
         *S = 4;
@@ -180,9 +185,17 @@ bool choose_shape(int N, int* S, int* NPL) {
         return true;
       }
   }
-  for (int v : npl8)
-    if (8 * v >= N) {
-      *S = 8;
+  if ((force == 0 && N <= 40) || force == 8) {
+    for (int v : npl8)
+      if (8 * v >= N) {
+        *S = 8;
+        *NPL = v;
+        return true;
+      }
+  }
+  for (int v : npl16)
+    if (16 * v >= N) {
+      *S = 16;
       *NPL = v;
       return true;
     }
@@ -288,7 +301,7 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
   b.d_delta = io->d_delta;
   b.d_u = io->d_u;
   b.part_bc = static_cast<float*>(io->work);
-  b.part_par = reinterpret_cast<float*>(static_cast<char*>(io->work) + pl.part_bc_bytes);
+  b.part_par = reinterpret_cast<double*>(static_cast<char*>(io->work) + pl.part_bc_bytes);
   b.bg = pl.bg;
   b.nbg = pl.nbg;
   hipStream_t s = (hipStream_t)stream;

@@ -130,12 +130,32 @@ __device__ __forceinline__ float reduce_states(float v) {
   return v;
 }
 
-// Sum over the DT channels of a wave that share slice s (lanes s, s+S, ...).
+// Sum over the channels of one 16-lane row that share slice s (lanes
+// s, s+S, ... of the row), with DPP row rotations on the VALU.  Every lane
+// of the row ends with the total of its slice; the order of the additions is
+// fixed, so the result is deterministic.
 template <int S>
-__device__ __forceinline__ float reduce_channels(float v) {
-#pragma unroll
-  for (int m = S; m < kWave; m <<= 1) v = v + __shfl_xor(v, m, kWave);
+__device__ __forceinline__ float reduce_row(float v) {
+  static_assert(S == 2 || S == 4 || S == 8 || S == 16, "S must divide a 16-lane row");
+  if (S <= 8) v = v + dpp<0x128>(v);  // row_ror:8
+  if (S <= 4) v = v + dpp<0x124>(v);  // row_ror:4
+  if (S <= 2) v = v + dpp<0x122>(v);  // row_ror:2
   return v;
+}
+
+// Gate and e*sin of state j for lane slice s (backward).  Tracking and pad
+// states return pa (tanh(theta), or 0 for pad) with es = 0.
+template <int S>
+__device__ __forceinline__ float gate_es_of(int j, int s, int NR, bool has_imag, float dt,
+                                            float pa, float pb, float& es) {
+  if (j * S >= NR) {
+    es = 0.f;
+    return pa;
+  }
+  const float gr = rot_gate_es(dt, pa, pb, has_imag, es);
+  if ((j + 1) * S <= NR || j * S + s < NR) return gr;
+  es = 0.f;
+  return pa;
 }
 
 }  // namespace rp

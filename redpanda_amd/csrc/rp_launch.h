@@ -50,8 +50,8 @@ struct BwdIO {
   float* d_u;
   float* d_h0;       // (B, D, N) or null
   float* d_beta0;
-  float* part_bc;   // [2][ntiles][B][L][N]  per-tile dB / dC partial sums
-  float* part_par;  // [nbg][2][D][N]        per-batch-group dA partial sums
+  float* part_bc;    // [2][ntiles][B][L][N]  per-tile dB / dC partial sums
+  double* part_par;  // [nbg][2][D][N]        per-batch-group dA partial sums
   int bg;           // batch rows per workgroup
   int nbg;          // ceil(B / bg)
 };
@@ -92,6 +92,8 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 }  // namespace rp
 
 // Compiled (S, NPL) shapes: S lanes per channel, NPL states per lane.
+// d_state <= 20 uses 4 lanes per channel, <= 40 uses 8, <= 128 uses 16.
 #define RP_FOR_EACH_SHAPE(X) \
-  X(4, 1) X(4, 2) X(4, 3) X(4, 4) X(4, 5) X(4, 6) X(4, 8) X(4, 10) \
-  X(8, 6) X(8, 8) X(8, 9) X(8, 10) X(8, 12) X(8, 16)
+  X(4, 1) X(4, 2) X(4, 3) X(4, 4) X(4, 5) \
+  X(8, 3) X(8, 4) X(8, 5) \
+  X(16, 3) X(16, 4) X(16, 5) X(16, 6) X(16, 8)

@@ -13,14 +13,19 @@
 //     rot:   dAr += dg dt g,   dAi -= dg dt e sin,   ddt += dg (Ar g - Ai e sin)
 //     track: dTk += dg
 //
-// Work split: one workgroup = CB channels x a group of `bg` batch rows; each
-// lane keeps its states' parameter gradients in registers across the whole
-// group.  The forward stored the state entering every kCkptK-step chunk; the
-// backward walks chunks in reverse, recomputes the chunk's K states into
-// registers, then runs the adjoint over them.  Channel sums (dB, dC) reduce
-// across the wave with a butterfly, across the 4 waves through LDS, and
-// across workgroups as per-tile partials summed by the finalize kernel.
-// Every reduction has a fixed order: results are run-to-run deterministic.
+// Work split: one workgroup = CB channels x a group of `bg` batch rows, both
+// directions.  The forward stored the state entering every kCkptK-step chunk;
+// the backward walks chunks in reverse, recomputes the chunk's K steps into
+// registers (keeping s_{t-1}, the gate and e*sin, so the adjoint evaluates
+// no transcendental), then runs the adjoint over them.
+//
+// Reductions, all in a fixed order (run-to-run deterministic, no atomics):
+//   * over a channel's states (ddt, du): in-lane FMA chain + DPP butterfly;
+//   * over channels (dB, dC): DPP row rotations inside each 16-lane row, the
+//     row partials staged in LDS, then a 16-way sum per output, per tile;
+//     the per-tile partials are summed in float64 by a second kernel;
+//   * parameter gradients (dA, dTk): 8-step fp32 chunk sums accumulated in
+//     float64 per lane over the batch group, then float64 across groups.
 
 #include "rp_device.h"
 #include "rp_launch.h"
@@ -28,35 +33,41 @@
 namespace rp {
 
 template <int S, int NPL>
-__global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO io) {
+__global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, BwdIO io) {
   using Sh = Shape<S, NPL>;
   constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = kBwdTB, K = kCkptK;
-  static_assert(TB % K == 0, "time block must hold whole chunks");
+  constexpr int KR = NP <= 40 ? K : K / 2;  // steps per channel-sum fold
+  constexpr int NRW = kWaves * 4;           // 16-lane rows per workgroup
+  static_assert(TB % K == 0 && K % KR == 0, "time block must hold whole chunks");
   // row 0 = the step just before the block (its (dt*u)/2 and B seed the
   // trapezoid carry at the first chunk's entry); rows 1..TB = the block
-  __shared__ float4 sCh[TB + 1][CB];      // (dt, (dt*u)/2, u, dy)
+  __shared__ float4 sCh[TB + 1][CB];        // (dt, (dt*u)/2, u, dy)
   __shared__ float sB[TB + 1][NP];
   __shared__ float sC[TB + 1][NP];
-  __shared__ float sRed[kWaves][K][2][NP]; // per-wave channel sums of a chunk
+  __shared__ float sRed[KR][2][NRW][NP];    // per-row channel sums of dB, dC
+  __shared__ float2 sDD[TB][CB];            // (d_delta, d_u) of the block
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
   const int dl = lane / S, s = lane % S;
   const int cl = wave * DT + dl;
+  const int wrow = wave * 4 + lane / 16;    // row index within the workgroup
+  const bool row_leader = (lane % 16) < S;  // first channel of its row
   const int tile = blockIdx.x % p.ntiles, bgi = blockIdx.x / p.ntiles;
   const int c = tile * CB + cl;
   const bool cvalid = c < p.D;
   const bool has_imag = p.Ai != nullptr;
   const int L = p.L;
 
-  float pa[NPL], pb[NPL], dpa[NPL], dpb[NPL];
+  float pa[NPL], pb[NPL];
+  double dpa[NPL], dpb[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int n = j * S + s;
     pa[j] = 0.f;
     pb[j] = 0.f;
-    dpa[j] = 0.f;
-    dpb[j] = 0.f;
+    dpa[j] = 0.0;
+    dpb[j] = 0.0;
     if (cvalid && n < p.NR) {
       pa[j] = p.Ar[(int64_t)c * p.NR + n] * kLog2e;
       if (has_imag) pb[j] = p.Ai[(int64_t)c * p.NR + n] * kInv2Pi;
@@ -152,8 +163,8 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO 
               hbp[j] = fmul(hdp, sB[m0][s * NPL + j]);
             }
           }
-          // recompute: traj[m][j] = s_{t-1} (the value the gate multiplies)
-          float traj[K][NPL];
+          // recompute the chunk: s_{t-1}, g_t and e*sin for every step
+          float SP[K][NPL], G[K][NPL], ES[K][NPL];
 #pragma unroll
           for (int m = 0; m < K; ++m) {
             if (m < kcnt) {
@@ -162,18 +173,20 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO 
               const float hd = sCh[row][cl].y;
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
-                const float g = gate_of<S>(j, s, p.NR, has_imag, dt, pa[j], pb[j]);
+                float es;
+                const float g = gate_es_of<S>(j, s, p.NR, has_imag, dt, pa[j], pb[j], es);
                 const float hb = fmul(hd, sB[row][s * NPL + j]);
                 const float sm = hc[j] + hbp[j];
-                traj[m][j] = sm;
+                SP[m][j] = sm;
+                G[m][j] = g;
+                ES[m][j] = es;
                 hc[j] = ffma(g, sm, hb);
                 hbp[j] = hb;
               }
             }
           }
           // adjoint over the chunk, last step first.  Parameter gradients sum
-          // into chunk-local accumulators first (two-level summation keeps
-          // the in-lane error at O(K + L/K) roundings instead of O(L)).
+          // into chunk-local fp32 accumulators, then into float64.
           float cpa[NPL], cpb[NPL];
 #pragma unroll
           for (int j = 0; j < NPL; ++j) {
@@ -187,7 +200,6 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO 
               const float4 ch = sCh[row][cl];
               const float dt = ch.x, hd = ch.y, uu = ch.z, dy = ch.w;
               float ddA = 0.f, ddB = 0.f, sBc = 0.f;
-              float xB[NPL], xC[NPL];
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
                 const float Bv = sB[row][s * NPL + j];
@@ -195,22 +207,16 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO 
                 const bool all_rot = (j + 1) * S <= p.NR;
                 const bool all_trk = j * S >= p.NR;
                 const bool rot = all_rot || (!all_trk && (j * S + s < p.NR));
-                float g, es = 0.f;
-                if (all_trk) {
-                  g = pa[j];
-                } else {
-                  const float gr = rot_gate_es(dt, pa[j], pb[j], has_imag, es);
-                  g = rot ? gr : pa[j];
-                }
+                const float g = G[m][j];
                 const float hb = fmul(hd, Bv);
-                const float ht = ffma(g, traj[m][j], hb);
+                const float ht = ffma(g, SP[m][j], hb);
                 const float q = ffma(dy, Cv, gq[j]);
                 const float dhb = q + gr[j];
                 sBc = ffma(dhb, Bv, sBc);
-                const float dg = fmul(q, traj[m][j]);
+                const float dg = fmul(q, SP[m][j]);
                 if (rot) {
                   const float t1 = fmul(dg, g);
-                  const float t2 = fmul(dg, es);
+                  const float t2 = fmul(dg, ES[m][j]);
                   cpa[j] = ffma(t1, dt, cpa[j]);
                   cpb[j] = ffma(t2, dt, cpb[j]);
                   ddA = ffma(pa[j], t1, ddA);
@@ -220,68 +226,72 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO 
                 }
                 gq[j] = fmul(g, q);
                 gr[j] = gq[j];
-                xC[j] = fmul(dy, ht);
-                xB[j] = fmul(dhb, hd);
+                const float xB = reduce_row<S>(fmul(dhb, hd));
+                const float xC = reduce_row<S>(fmul(dy, ht));
+                if (row_leader) {
+                  sRed[m % KR][0][wrow][s * NPL + j] = xB;
+                  sRed[m % KR][1][wrow][s * NPL + j] = xC;
+                }
               }
               ddA = reduce_states<S>(ddA);
               ddB = reduce_states<S>(ddB);
               sBc = reduce_states<S>(sBc);
-              const int i = i0 + m0 + m;
-              const int t = dir ? (L - 1 - i) : i;
-              if (s == 0 && cvalid) {
+              if (s == 0) {
                 const float ddt = ffma(kLn2, ddA, -fmul(kTwoPi, ddB)) + fmul(0.5f * uu, sBc);
                 const float dut = fmul(0.5f * dt, sBc);
-                const int64_t idx = ((int64_t)b * L + t) * p.D + c;
-                if (dir == 0) {
-                  io.d_delta[idx] = ddt;
-                  io.d_u[idx] = dut;
-                } else {
-                  io.d_delta[idx] = io.d_delta[idx] + ddt;
-                  io.d_u[idx] = io.d_u[idx] + dut;
+                sDD[m0 + m][cl] = make_float2(ddt, dut);
+              }
+            }
+            if (m % KR == 0) {
+              // fold the 16 row partials of steps [m, m + KR) into this
+              // tile's global dB / dC partials
+              __syncthreads();
+              for (int e = tid; e < KR * 2 * p.N; e += kThreads) {
+                const int rr = e / (2 * p.N);
+                const int rem = e % (2 * p.N);
+                const int which = rem / p.N, n = rem % p.N;
+                if (m + rr < kcnt) {
+                  const int k = (n % S) * NPL + n / S;
+                  float v = sRed[rr][which][0][k];
+#pragma unroll
+                  for (int w = 1; w < NRW; ++w) v = v + sRed[rr][which][w][k];
+                  const int i = i0 + m0 + m + rr;
+                  const int t = dir ? (L - 1 - i) : i;
+                  float* dst = io.part_bc +
+                               (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
+                               (int64_t)t * p.N + n;
+                  if (dir == 0)
+                    *dst = v;
+                  else
+                    *dst = *dst + v;
                 }
               }
-#pragma unroll
-              for (int j = 0; j < NPL; ++j) {
-                xB[j] = reduce_channels<S>(xB[j]);
-                xC[j] = reduce_channels<S>(xC[j]);
-              }
-              if (dl == 0) {
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) {
-                  sRed[wave][m][0][s * NPL + j] = xB[j];
-                  sRed[wave][m][1][s * NPL + j] = xC[j];
-                }
-              }
+              __syncthreads();
             }
           }
 #pragma unroll
           for (int j = 0; j < NPL; ++j) {
-            dpa[j] = dpa[j] + cpa[j];
-            dpb[j] = dpb[j] + cpb[j];
+            dpa[j] += (double)cpa[j];
+            dpb[j] += (double)cpb[j];
           }
-          __syncthreads();
-          // fold the 4 waves' channel sums into this tile's global partials
-          for (int e = tid; e < kcnt * 2 * NP; e += kThreads) {
-            const int m = e / (2 * NP);
-            const int rem = e % (2 * NP);
-            const int which = rem / NP, k = rem % NP;
-            const int n = (k % NPL) * S + (k / NPL);
-            if (n < p.N) {
-              float v = sRed[0][m][which][k];
-#pragma unroll
-              for (int w = 1; w < kWaves; ++w) v = v + sRed[w][m][which][k];
-              const int i = i0 + m0 + m;
-              const int t = dir ? (L - 1 - i) : i;
-              float* dst = io.part_bc +
-                           (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
-                           (int64_t)t * p.N + n;
-              if (dir == 0)
-                *dst = v;
-              else
-                *dst = *dst + v;
+        }
+        // the block's (d_delta, d_u) rows, written channel-contiguous
+        for (int e = tid; e < cnt * CB; e += kThreads) {
+          const int r = e / CB, ci = e % CB;
+          const int c2 = tile * CB + ci;
+          if (c2 < p.D) {
+            const int i = i0 + r;
+            const int t = dir ? (L - 1 - i) : i;
+            const float2 v = sDD[r][ci];
+            const int64_t idx = ((int64_t)b * L + t) * p.D + c2;
+            if (dir == 0) {
+              io.d_delta[idx] = v.x;
+              io.d_u[idx] = v.y;
+            } else {
+              io.d_delta[idx] = io.d_delta[idx] + v.x;
+              io.d_u[idx] = io.d_u[idx] + v.y;
             }
           }
-          __syncthreads();
         }
       }
       // after the sweep gq = g_0 q_0: the gradient of the initial state, since
@@ -299,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void scan_bwd_kernel(ScanParams p, BwdIO 
       }
     }
   }
-  // per-batch-group parameter-gradient partials
+  // per-batch-group parameter-gradient partials (float64)
   if (cvalid) {
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
@@ -325,8 +335,8 @@ __global__ void bwd_reduce_bc(const float* __restrict__ part, float* __restrict_
   (which ? dC : dB)[k] = (float)acc;
 }
 
-// dA_real / dA_imag / dtrack: sum the per-batch-group partials (fp64).
-__global__ void bwd_reduce_par(const float* __restrict__ part, float* __restrict__ dAr,
+// dA_real / dA_imag / dtrack: sum the per-batch-group float64 partials.
+__global__ void bwd_reduce_par(const double* __restrict__ part, float* __restrict__ dAr,
                                float* __restrict__ dAi, float* __restrict__ dTk, int D, int N,
                                int NR, int nbg) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -374,7 +384,7 @@ hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc
   const int64_t dn = (int64_t)p.D * p.N;
   if (dn > 0) {
     hipLaunchKernelGGL(bwd_reduce_par, dim3((unsigned)((dn + 255) / 256)), dim3(256), 0, st,
-                       (const float*)io.part_par, d_Ar, d_Ai, d_Tk, p.D, p.N, p.NR, io.nbg);
+                       (const double*)io.part_par, d_Ar, d_Ai, d_Tk, p.D, p.N, p.NR, io.nbg);
     return hipGetLastError();
   }
   return hipSuccess;

@@ -40,14 +40,20 @@ def _pair(cfg_kw, seed=0, perturb=True):
     hm = _hip()
     torch.manual_seed(seed)
     ref = model_ref.Mamba(model_ref.MambaConfig(**cfg_kw))
-    if perturb:  # move A / theta off their structured init so every lane matters
+    if perturb:
+        # move A / theta off their structured init so every lane matters, while
+        # keeping Re(A) = -exp(log_mag) cos(phase) < 0 (|phase| < pi/2): a
+        # positive real part makes exp(dt Re A) > 1 and the scan grow without
+        # bound, which no fp32 implementation reproduces
         gen = torch.Generator().manual_seed(seed + 1)
         with torch.no_grad():
             for layer in ref.layers:
                 mx = layer["mixer"]
                 if hasattr(mx, "A_phase"):
-                    mx.A_phase.copy_((torch.rand(mx.A_phase.shape, generator=gen) * 2 - 1) * math.pi)
-                    mx.A_log_mag.copy_(torch.rand(mx.A_log_mag.shape, generator=gen) * 2.0)
+                    mx.A_phase.copy_((torch.rand(mx.A_phase.shape, generator=gen) * 2 - 1) * 1.4)
+                    mx.A_log_mag.copy_(torch.rand(mx.A_log_mag.shape, generator=gen) * 3.0 - 1.0)
+                if hasattr(mx, "A_log"):
+                    mx.A_log.copy_(torch.rand(mx.A_log.shape, generator=gen) * 3.0 - 1.0)
                 if hasattr(mx, "track_theta"):
                     mx.track_theta.copy_(torch.randn(mx.track_theta.shape, generator=gen) * 1.5)
     hip = hm.Mamba(hm.MambaConfig(**cfg_kw))
@@ -69,19 +75,26 @@ def _compare_train_step(cfg_kw, B, L, seed, tag):
     ref64.load_state_dict(ref.state_dict())
     gen = torch.Generator().manual_seed(seed + 7)
     ids = torch.randint(0, cfg_kw["vocab_size"], (B, L), generator=gen).to(dev)
+    # upstream gradient dout ~ N(0, 1): a loss whose gradient is not a
+    # cancellation residue (mean(norm_f(x)^2) is nearly constant in x)
+    dout = torch.randn(B, L, cfg_kw["d_model"], generator=gen).to(dev)
     outs = {}
     for name, m in (("hip", hip), ("ref", ref), ("f64", ref64)):
         m.train()
         y = m(ids)
-        y.pow(2).mean().backward()
+        (y * dout.to(y.dtype)).sum().backward()
         outs[name] = (y.detach(), _grads(m))
     (yh, gh), (yr, gr), (y64, g64) = outs["hip"], outs["ref"], outs["f64"]
     rep = {"y": (rel(yh, yr), rel(yh, y64), rel(yr, y64))}
     for k in gr:
         rep[k] = (rel(gh[k], gr[k]), rel(gh[k], g64[k]), rel(gr[k], g64[k]))
     worst = max(rep.items(), key=lambda kv: kv[1][0])
-    print(tag, f"y {rep['y'][0]:.1e}; worst grad {worst[0]} {worst[1][0]:.1e} "
-               f"(hip-f64 {worst[1][1]:.1e}, ref-f64 {worst[1][2]:.1e})", flush=True)
+    print(tag, "y (hip-ref, hip-f64, ref-f64) = (%.1e %.1e %.1e)" % rep["y"],
+          f"worst grad {worst[0]} {worst[1][0]:.1e} "
+          f"(hip-f64 {worst[1][1]:.1e}, ref-f64 {worst[1][2]:.1e})", flush=True)
+    for k, v in rep.items():
+        if k != "y":
+            print(f"   {k}: %.1e %.1e %.1e" % v)
     assert within_bar(*rep.pop("y"), FWD_TOL), tag
     for k, v in rep.items():
         assert within_bar(*v, GRAD_TOL), f"{tag}: {k} (hip-ref, hip-f64, ref-f64) = {v}"
@@ -109,10 +122,38 @@ def test_eval_mamba_12_layers_end_to_end(gpu_lib):
     _compare_train_step(cfg, B=8, L=64, seed=3, tag="eval-mamba 12L")
 
 
+def _f64_arbiter(g, bidir):
+    """The oracle's restatement of the fixture model in float64 on the CPU:
+    the arbiter for cross-device comparisons (fixture weights put half the
+    rotational gates above 1, so the fp32 results carry amplified rounding)."""
+    cfg = model_ref.MambaConfig(d_model=16, n_layer=2, d_state=12, n_track_state=4, mimo_p=2,
+                                vocab_size=64, bidirectional=bidir)
+    m = model_ref.Mamba(cfg).double()
+    m.load_state_dict({k[3:]: v.double() if v.is_floating_point() else v
+                       for k, v in g.items() if k.startswith("sd.")})
+    m.train()
+    y = m(g["ids"])
+    y.pow(2).mean().backward()
+    return y.detach(), {k: p.grad for k, p in m.named_parameters() if p.grad is not None}
+
+
+XDEV_TOL = 1e-5  # GPU GEMMs vs the fixture's CPU GEMMs
+
+
+def fixture_grad_ok(e_hip_ref, e_hip_64, e_ref_64):
+    """Gradient check against a fixture whose loss is a near-cancellation
+    (mean(norm_f(x)^2), mean of LayerNorm-ed logits): its gradients are
+    rounding residues at the 1e-6..1e-5 level in any fp32 implementation,
+    so beyond 1e-5 of the fixture the HIP result must stay within twice the
+    fixture's own distance from the float64 arbiter."""
+    return e_hip_ref <= XDEV_TOL or e_hip_64 <= 2.0 * max(XDEV_TOL, e_ref_64)
+
+
 @pytest.mark.parametrize("bidir", [False, True])
 def test_golden_model_fixture(gpu_lib, bidir):
-    """The reference's own CPU outputs and gradients (cross-device: GEMMs on
-    the GPU vs the CPU, so the bar here is 1e-5 for outputs and gradients)."""
+    """The reference's own CPU outputs and gradients.  Cross-device (GEMMs on
+    the GPU vs the CPU): each tensor is within 1e-5 of the fixture, or no
+    further from the float64 arbiter than the fixture itself is."""
     hm = _hip()
     g = load_golden(f"model_bi{int(bidir)}")
     cfg = hm.MambaConfig(d_model=16, n_layer=2, d_state=12, n_track_state=4, mimo_p=2,
@@ -124,26 +165,32 @@ def test_golden_model_fixture(gpu_lib, bidir):
     m.to(dev).train()
     ids = g["ids"].to(dev)
     y = m(ids)
-    assert rel(y, g["y_train"]) <= 1e-5
     y.pow(2).mean().backward()
-    for k, p in m.named_parameters():
-        if "grad." + k in g:
-            assert rel(p.grad, g["grad." + k]) <= 1e-5, k
+    y64, g64 = _f64_arbiter(g, bidir)
+    checks = [("y", y, g["y_train"], y64)]
+    checks += [(k, p.grad, g["grad." + k], g64[k]) for k, p in m.named_parameters()
+               if "grad." + k in g]
+    k, a, ref, r64 = checks.pop(0)
+    assert within_bar(rel(a, ref), rel(a, r64), rel(ref, r64), XDEV_TOL), "y"
+    for k, a, ref, r64 in checks:
+        e = (rel(a, ref), rel(a, r64), rel(ref, r64))
+        assert fixture_grad_ok(*e), f"{k}: (hip-ref, hip-f64, ref-f64) = {e}"
     m.eval()
     with torch.no_grad():
-        assert rel(m(ids), g["y_eval"]) <= 1e-5
+        assert rel(m(ids), g["y_eval"]) <= XDEV_TOL
         if not bidir:
             cache, outs = None, []
             for t in range(ids.shape[1]):
                 hdn, cache = m.step(token_id=ids[:, t], cache=cache)
                 outs.append(hdn)
-            assert rel(torch.stack(outs, 1), g["y_step"]) <= 1e-5
+            assert rel(torch.stack(outs, 1), g["y_step"]) <= XDEV_TOL
             fin, pc = m.prime_cache(ids[:, :20])
-            assert rel(fin, g["prime_final"]) <= 1e-5
+            assert rel(fin, g["prime_final"]) <= XDEV_TOL
             for i, (h, b) in enumerate(pc):
-                assert rel(h, g[f"prime_h{i}"]) <= 1e-5 and rel(b, g[f"prime_beta{i}"]) <= 1e-5
+                assert rel(h, g[f"prime_h{i}"]) <= XDEV_TOL
+                assert rel(b, g[f"prime_beta{i}"]) <= XDEV_TOL
             nxt, _ = m.step(token_id=ids[:, 20], cache=pc)
-            assert rel(nxt, g["prime_next"]) <= 1e-5
+            assert rel(nxt, g["prime_next"]) <= XDEV_TOL
 
 
 def test_model_step_equals_forward(gpu_lib):
@@ -173,58 +220,85 @@ def test_model_step_equals_forward(gpu_lib):
 def test_step_under_autograd_matches_reference(gpu_lib):
     """Training through step() (SearchMamba.dynamics_rollout pattern): prime
     on a prefix, step T moves with autograd on, gradients of every parameter
-    against the oracle on the same GPU."""
+    against the oracle on the same GPU (fp32 bars, float64 arbiter)."""
     cfg = dict(d_model=32, n_layer=2, d_state=12, n_track_state=4, mimo_p=2, vocab_size=200)
     hip, ref = _pair(cfg, seed=6)
+    ref64 = model_ref.Mamba(model_ref.MambaConfig(**cfg)).to(dev).double()
+    ref64.load_state_dict(ref.state_dict())
     gen = torch.Generator().manual_seed(8)
     board = torch.randint(0, 200, (3, 15), generator=gen).to(dev)
     moves = torch.randint(0, 200, (3, 5), generator=gen).to(dev)
+    proj = torch.randn(5, 3, 32, generator=gen).to(dev)
     res = {}
-    for name, m in (("hip", hip), ("ref", ref)):
+    for name, m in (("hip", hip), ("ref", ref), ("f64", ref64)):
         m.train()
         _, cache = m.prime_cache(board)
         loss = 0.0
         for t in range(moves.shape[1]):
             h, cache = m.step(token_id=moves[:, t], cache=cache)
-            loss = loss + h.pow(2).mean()
+            loss = loss + (h * proj[t].to(h.dtype)).sum()
         loss.backward()
         res[name] = (loss.detach(), _grads(m))
-    assert rel(res["hip"][0], res["ref"][0]) <= 1e-5
-    for k, gref in res["ref"][1].items():
-        e = rel(res["hip"][1][k], gref)
-        assert e <= 1e-5, f"{k}: {e:.2e}"
+    (lh, gh), (lr, gr), (l64, g64) = res["hip"], res["ref"], res["f64"]
+    assert within_bar(rel(lh, lr), rel(lh, l64), rel(lr, l64), FWD_TOL)
+    for k in gr:
+        e = (rel(gh[k], gr[k]), rel(gh[k], g64[k]), rel(gr[k], g64[k]))
+        assert within_bar(*e, GRAD_TOL), f"{k}: (hip-ref, hip-f64, ref-f64) = {e}"
+
+
+def _search_pair(g):
+    """The HIP SearchMamba on the GPU and a float64 arbiter on the CPU: the
+    same heads over the oracle's restated backbone."""
+    from redpanda_amd.search_mamba import SearchMamba, SearchMambaConfig
+    kw = dict(d_model=16, n_layer=2, d_state=8, n_track_state=2, mimo_p=2, vocab_size=64)
+    sd = {k[3:]: v for k, v in g.items() if k.startswith("sd.")}
+    sm = SearchMamba(SearchMambaConfig(**kw), vocab_size=64, eval_dim=12)
+    sm.load_state_dict(sd)
+    arb = SearchMamba(SearchMambaConfig(**kw), vocab_size=64, eval_dim=12)
+    arb.backbone = model_ref.Mamba(model_ref.MambaConfig(**kw))
+    arb.load_state_dict(sd)
+    return sm.to(dev), arb.double()
 
 
 def test_search_mamba_golden(gpu_lib):
     """SearchMamba on the reference's fixture: dynamics_rollout values and
     gradients, prime_board, eval_step, _expand_cache + batched step, and the
-    fast (prime + step) vs slow (full scan) line evaluation."""
-    from redpanda_amd.search_mamba import SearchMamba, SearchMambaConfig
+    fast (prime + step) vs slow (full scan) line evaluation.  Cross-device,
+    so each tensor is within 1e-5 of the fixture or no further from the
+    float64 arbiter than the fixture is."""
     g = load_golden("search")
-    cfg = SearchMambaConfig(d_model=16, n_layer=2, d_state=8, n_track_state=2, mimo_p=2,
-                            vocab_size=64)
-    sm = SearchMamba(cfg, vocab_size=64, eval_dim=12)
-    sm.load_state_dict({k[3:]: v for k, v in g.items() if k.startswith("sd.")})
-    sm.to(dev).train()
-    board, moves = g["board"].to(dev), g["moves"].to(dev)
-    v, c, f = sm.dynamics_rollout(board, moves)
-    assert rel(v, g["dyn_v"]) <= 1e-5 and rel(c, g["dyn_c"]) <= 1e-5 and rel(f, g["dyn_f"]) <= 1e-5
+    sm, arb = _search_pair(g)
+    sm.train()
+    arb.train()
+    board, moves = g["board"], g["moves"]
+    v, c, f = sm.dynamics_rollout(board.to(dev), moves.to(dev))
+    v64, c64, f64 = arb.dynamics_rollout(board, moves)
     (v.pow(2).mean() + c.mean() + f.pow(2).mean()).backward()
-    for k, p in sm.named_parameters():
-        if "grad." + k in g:
-            assert rel(p.grad, g["grad." + k]) <= 1e-5, k
+    (v64.pow(2).mean() + c64.mean() + f64.pow(2).mean()).backward()
+    checks = [("dyn_v", v, g["dyn_v"], v64), ("dyn_c", c, g["dyn_c"], c64),
+              ("dyn_f", f, g["dyn_f"], f64)]
+    g64 = dict(arb.named_parameters())
+    checks += [(k, p.grad, g["grad." + k], g64[k].grad) for k, p in sm.named_parameters()
+               if "grad." + k in g]
+    for k, a, ref, r64 in checks[:3]:
+        assert within_bar(rel(a, ref), rel(a, r64), rel(ref, r64), XDEV_TOL), k
+    for k, a, ref, r64 in checks[3:]:
+        e = (rel(a, ref), rel(a, r64), rel(ref, r64))
+        assert fixture_grad_ok(*e), f"{k}: (hip-ref, hip-f64, ref-f64) = {e}"
     sm.eval()
     with torch.no_grad():
-        fin, cache = sm.prime_board(board[0])
-        assert rel(fin, g["prime_final"]) <= 1e-5
-        val, cont, cache2 = sm.eval_step(cache, int(g["moves"][0, 0]))
-        assert abs(val - float(g["eval_value"][0])) <= 1e-5 * max(1.0, abs(float(g["eval_value"][0])))
-        assert rel(cont, g["eval_cont"]) <= 1e-5
+        b0 = board[0].to(dev)
+        fin, cache = sm.prime_board(b0)
+        assert rel(fin, g["prime_final"]) <= XDEV_TOL
+        val, cont, cache2 = sm.eval_step(cache, int(moves[0, 0]))
+        ev = float(g["eval_value"][0])
+        assert abs(val - ev) <= XDEV_TOL * max(1.0, abs(ev))
+        assert rel(cont, g["eval_cont"]) <= XDEV_TOL
         exp = sm._expand_cache(cache2, 4)
-        hB, _ = sm.backbone.step(token_id=moves[:, 1].repeat(2)[:4], cache=exp)
-        assert rel(hB, g["expand_step"]) <= 1e-5
-        assert rel(sm.evaluate_lines_fast(board[0], moves), g["lines_fast"]) <= 1e-5
-        assert rel(sm.evaluate_lines(board[0], moves), g["lines_slow"]) <= 1e-5
+        hB, _ = sm.backbone.step(token_id=moves[:, 1].repeat(2)[:4].to(dev), cache=exp)
+        assert rel(hB, g["expand_step"]) <= XDEV_TOL
+        assert rel(sm.evaluate_lines_fast(b0, moves.to(dev)), g["lines_fast"]) <= XDEV_TOL
+        assert rel(sm.evaluate_lines(b0, moves.to(dev)), g["lines_slow"]) <= XDEV_TOL
 
 
 def test_cpu_tensors_are_refused(gpu_lib):
