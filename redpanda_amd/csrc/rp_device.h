@@ -11,10 +11,22 @@
 // an in-lane FMA chain over j followed by a DPP butterfly over the S lanes;
 // the step kernel uses the very same functions, so step == scan bit for bit.
 //
-// Gate arithmetic uses the gfx950 transcendental unit directly:
-//     exp(dt*Ar)  = v_exp_f32(dt * (Ar*log2 e))
-//     cos(dt*Ai)  = v_cos_f32(fract(|dt * (Ai/2pi)|))   (input in revolutions)
-// fract(|x|) is exact and keeps v_cos_f32 inside its valid input domain.
+// Gate arithmetic (rot_gate below).  exp uses the transcendental unit
+// (v_exp_f32 is good to 0.8 ulp and unbiased); cos / sin do not: measured on
+// gfx950, v_cos_f32 / v_sin_f32 are off by up to ~2 ulp with a bias of
+// +-0.3..0.6 ulp that depends on the angle (-0.6 ulp near cos = 1).  A gate
+// close to 1 carries state over tens of steps, so a biased gate turns into a
+// relative drift of the state of ~(steps x bias) and a visible error in the
+// gradients that sum over steps.  The rotational gate is therefore
+// evaluated to ~1 ulp without systematic bias:
+//     exp(dt*Ar)  = 2^(x log2 e), x = fl(dt*Ar) as the reference rounds it,
+//                   the rounding error of x*log2e folded back;
+//     cos / sin   of the angle in revolutions w = dt*(wh + wl), where
+//                   wh + wl = Ai/(2 pi) to 2^-48, reduced exactly to a
+//                   16-entry table and |x| <= pi/16, where short Taylor
+//                   polynomials are accurate to < 1e-9.
+// The forward, the step and the backward's recompute share the code, so the
+// backward recomputes exactly the gates the forward used.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -26,10 +38,10 @@
 namespace rp {
 
 constexpr float kLog2e = 1.44269504088896340736f;
-constexpr float kInv2Pi = 0.15915494309189533577f;
+constexpr float kLog2eLo = 1.925963e-08f;  // log2(e) - float(log2(e))
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kTwoPi = 6.28318530717958647692f;
-
+constexpr double kInv2PiD = 0.15915494309189533577;
 
 template <int S, int NPL>
 struct Shape {
@@ -57,38 +69,94 @@ __device__ __forceinline__ float ffma(float a, float b, float c) { return __buil
 // exp2 on the transcendental unit (v_exp_f32).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Rotational gate exp(dt*Ar) * cos(dt*Ai) with pa = Ar*log2e, pb = Ai/(2pi).
-__device__ __forceinline__ float rot_gate(float dt, float pa, float pb, bool has_imag) {
-  const float e = exp2_hw(fmul(dt, pa));
-  if (!has_imag) return e;
-  const float r = __builtin_amdgcn_fractf(__builtin_fabsf(fmul(dt, pb)));
-  return fmul(e, __builtin_amdgcn_cosf(r));
+// cos / sin of 2 pi k / 16, k = 0..15 (filled into LDS once per workgroup).
+__device__ __forceinline__ void sincos_table_entry(int k, float& c, float& s) {
+  constexpr float kC1 = 0.923879532511286756f, kC2 = 0.707106781186547524f,
+                  kC3 = 0.382683432365089772f;
+  const float cq[4] = {1.f, kC1, kC2, kC3};  // cos of 0, 1/16, 2/16, 3/16 rev
+  const int q = (k >> 2) & 3, r = k & 3;
+  const float c0 = cq[r];
+  const float s0 = (r == 0) ? 0.f : cq[(4 - r) & 3];
+  c = (q == 0) ? c0 : (q == 1) ? -s0 : (q == 2) ? -c0 : s0;
+  s = (q == 0) ? s0 : (q == 1) ? c0 : (q == 2) ? -s0 : -c0;
 }
 
-// Rotational gate plus e*sin(dt*Ai) for the backward (dg/dAi, dg/ddt).
-__device__ __forceinline__ float rot_gate_es(float dt, float pa, float pb, bool has_imag,
-                                             float& es) {
-  const float e = exp2_hw(fmul(dt, pa));
+__device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
+  if (tid < 16) {
+    float c, s;
+    sincos_table_entry(tid, c, s);
+    tab[tid] = make_float2(c, s);
+  }
+}
+
+// Per-state gate parameters held in registers: ar = A_real (rotational) or
+// tanh(theta) (tracking; 0 for pad states), wh + wl = A_imag / (2 pi).
+__device__ __forceinline__ void load_gate_params(const float* Ar, const float* Ai, const float* Tk,
+                                                 int c, int n, int N, int NR, int NT, bool valid,
+                                                 float& ar, float& wh, float& wl) {
+  ar = 0.f;
+  wh = 0.f;
+  wl = 0.f;
+  if (!valid) return;
+  if (n < NR) {
+    ar = Ar[(int64_t)c * NR + n];
+    if (Ai != nullptr) {
+      const double w = (double)Ai[(int64_t)c * NR + n] * kInv2PiD;
+      wh = (float)w;
+      wl = (float)(w - (double)wh);
+    }
+  } else if (n < N) {
+    ar = Tk[(int64_t)c * NT + (n - NR)];
+  }
+}
+
+// Rotational gate g = exp(dt*ar) cos(2 pi dt (wh + wl)); with WITH_SIN also
+// es = exp(dt*ar) sin(...) for the backward.  The cos path is the same code
+// in both instantiations, so g is bitwise the same.
+template <bool WITH_SIN>
+__device__ __forceinline__ float rot_gate(float dt, float ar, float wh, float wl, bool has_imag,
+                                          const float2* tab, float& es) {
+  const float x = fmul(dt, ar);
+  const float p = fmul(x, kLog2e);
+  const float perr = ffma(x, kLog2eLo, ffma(x, kLog2e, -p));
+  const float e0 = exp2_hw(p);
+  const float e = ffma(e0, fmul(perr, kLn2), e0);
   if (!has_imag) {
     es = 0.f;
     return e;
   }
-  const float w = fmul(dt, pb);
-  const float r = __builtin_amdgcn_fractf(__builtin_fabsf(w));
-  const float sn = __builtin_copysignf(__builtin_amdgcn_sinf(r), w);
-  es = fmul(e, sn);
-  return fmul(e, __builtin_amdgcn_cosf(r));
+  const float w = fmul(dt, wh);
+  const float wlo = ffma(dt, wl, ffma(dt, wh, -w));
+  const float kf = __builtin_rintf(fmul(w, 16.f));
+  const float rr = ffma(kf, -0.0625f, w) + wlo;  // exact reduction, |rr| <= 1/32
+  const float xr = fmul(rr, kTwoPi);
+  const float x2 = fmul(xr, xr);
+  const float cm1 = fmul(x2, ffma(x2, ffma(x2, -1.f / 720.f, 1.f / 24.f), -0.5f));  // cos - 1
+  const float sx = ffma(fmul(xr, x2), ffma(x2, 1.f / 120.f, -1.f / 6.f), xr);        // sin
+  const float2 cs = tab[(int)kf & 15];
+  const float cv = ffma(-cs.y, sx, ffma(cs.x, cm1, cs.x));
+  if (WITH_SIN) {
+    const float sv = ffma(cs.x, sx, ffma(cs.y, cm1, cs.y));
+    es = fmul(e, sv);
+  } else {
+    es = 0.f;
+  }
+  return fmul(e, cv);
 }
 
 // Gate of state j for lane slice s: rotational if n < NR, else the tracking
-// gate pa = tanh(theta) (pad states beyond N carry pa = 0 and B = C = 0).
-template <int S>
-__device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pa,
-                                         float pb) {
-  if ((j + 1) * S <= NR) return rot_gate(dt, pa, pb, has_imag);
-  if (j * S >= NR) return pa;
-  const float gr = rot_gate(dt, pa, pb, has_imag);
-  return (j * S + s < NR) ? gr : pa;
+// gate ar = tanh(theta) (pad states beyond N carry ar = 0 and B = C = 0).
+template <int S, bool WITH_SIN>
+__device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float ar,
+                                         float wh, float wl, const float2* tab, float& es) {
+  if (j * S >= NR) {
+    es = 0.f;
+    return ar;
+  }
+  const float gr = rot_gate<WITH_SIN>(dt, ar, wh, wl, has_imag, tab, es);
+  if ((j + 1) * S <= NR || j * S + s < NR) return gr;
+  es = 0.f;
+  return ar;
 }
 
 // One recurrence step for the lane's NPL states; returns the lane's partial
@@ -97,14 +165,16 @@ __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, fl
 // previous step's hb.  Shared verbatim by the scan and step kernels.
 template <int S, int NPL>
 __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
-                                            const float (&pa)[NPL], const float (&pb)[NPL],
-                                            float dt, float hdu, const float* __restrict__ Bs,
+                                            const float (&ar)[NPL], const float (&wh)[NPL],
+                                            const float (&wl)[NPL], const float2* tab, float dt,
+                                            float hdu, const float* __restrict__ Bs,
                                             const float* __restrict__ Cs, int s, int NR,
                                             bool has_imag) {
   float y = 0.f;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const float g = gate_of<S>(j, s, NR, has_imag, dt, pa[j], pb[j]);
+    float unused;
+    const float g = gate_of<S, false>(j, s, NR, has_imag, dt, ar[j], wh[j], wl[j], tab, unused);
     const float hb = fmul(hdu, Bs[j]);
     const float sm = h[j] + hbp[j];
     h[j] = ffma(g, sm, hb);
@@ -141,21 +211,6 @@ __device__ __forceinline__ float reduce_row(float v) {
   if (S <= 4) v = v + dpp<0x124>(v);  // row_ror:4
   if (S <= 2) v = v + dpp<0x122>(v);  // row_ror:2
   return v;
-}
-
-// Gate and e*sin of state j for lane slice s (backward).  Tracking and pad
-// states return pa (tanh(theta), or 0 for pad) with es = 0.
-template <int S>
-__device__ __forceinline__ float gate_es_of(int j, int s, int NR, bool has_imag, float dt,
-                                            float pa, float pb, float& es) {
-  if (j * S >= NR) {
-    es = 0.f;
-    return pa;
-  }
-  const float gr = rot_gate_es(dt, pa, pb, has_imag, es);
-  if ((j + 1) * S <= NR || j * S + s < NR) return gr;
-  es = 0.f;
-  return pa;
 }
 
 }  // namespace rp

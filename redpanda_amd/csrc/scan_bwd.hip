@@ -17,7 +17,9 @@
 // directions.  The forward stored the state entering every kCkptK-step chunk;
 // the backward walks chunks in reverse, recomputes the chunk's K steps into
 // registers (keeping s_{t-1}, the gate and e*sin, so the adjoint evaluates
-// no transcendental), then runs the adjoint over them.
+// no transcendental), then runs the adjoint over them.  The recompute calls
+// the forward's gate code (with the sine added), so it rebuilds the forward's
+// states exactly.
 //
 // Reductions, all in a fixed order (run-to-run deterministic, no atomics):
 //   * over a channel's states (ddt, du): in-lane FMA chain + DPP butterfly;
@@ -46,6 +48,7 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
   __shared__ float sC[TB + 1][NP];
   __shared__ float sRed[KR][2][NRW][NP];    // per-row channel sums of dB, dC
   __shared__ float2 sDD[TB][CB];            // (d_delta, d_u) of the block
+  __shared__ float2 sTab[16];               // cos, sin of 2 pi k / 16
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
@@ -59,21 +62,15 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
   const bool has_imag = p.Ai != nullptr;
   const int L = p.L;
 
-  float pa[NPL], pb[NPL];
+  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
+  // ar: A_real (rotational) or tanh(theta) (tracking); wh + wl: A_imag/(2 pi)
+  float ar[NPL], wh[NPL], wl[NPL];
   double dpa[NPL], dpb[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    const int n = j * S + s;
-    pa[j] = 0.f;
-    pb[j] = 0.f;
+    load_gate_params(p.Ar, p.Ai, p.Tk, c, j * S + s, p.N, p.NR, p.NT, cvalid, ar[j], wh[j], wl[j]);
     dpa[j] = 0.0;
     dpb[j] = 0.0;
-    if (cvalid && n < p.NR) {
-      pa[j] = p.Ar[(int64_t)c * p.NR + n] * kLog2e;
-      if (has_imag) pb[j] = p.Ai[(int64_t)c * p.NR + n] * kInv2Pi;
-    } else if (cvalid && n < p.N) {
-      pa[j] = p.Tk[(int64_t)c * p.NT + (n - p.NR)];
-    }
   }
 
   const int b_lo = bgi * io.bg;
@@ -174,7 +171,8 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
                 float es;
-                const float g = gate_es_of<S>(j, s, p.NR, has_imag, dt, pa[j], pb[j], es);
+                const float g = gate_of<S, true>(j, s, p.NR, has_imag, dt, ar[j], wh[j], wl[j],
+                                                 sTab, es);
                 const float hb = fmul(hd, sB[row][s * NPL + j]);
                 const float sm = hc[j] + hbp[j];
                 SP[m][j] = sm;
@@ -219,8 +217,8 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
                   const float t2 = fmul(dg, ES[m][j]);
                   cpa[j] = ffma(t1, dt, cpa[j]);
                   cpb[j] = ffma(t2, dt, cpb[j]);
-                  ddA = ffma(pa[j], t1, ddA);
-                  ddB = ffma(pb[j], t2, ddB);
+                  ddA = ffma(ar[j], t1, ddA);
+                  ddB = ffma(wh[j], t2, ddB);
                 } else {
                   cpa[j] = cpa[j] + dg;
                 }
@@ -237,7 +235,7 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
               ddB = reduce_states<S>(ddB);
               sBc = reduce_states<S>(sBc);
               if (s == 0) {
-                const float ddt = ffma(kLn2, ddA, -fmul(kTwoPi, ddB)) + fmul(0.5f * uu, sBc);
+                const float ddt = (ddA - fmul(kTwoPi, ddB)) + fmul(0.5f * uu, sBc);
                 const float dut = fmul(0.5f * dt, sBc);
                 sDD[m0 + m][cl] = make_float2(ddt, dut);
               }

@@ -25,6 +25,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   __shared__ float2 sDH[TB][CB];   // (dt, (dt*u)/2) per step and channel
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
+  __shared__ float2 sTab[16];      // cos, sin of 2 pi k / 16
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
@@ -36,19 +37,11 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   const bool has_imag = p.Ai != nullptr;
   const int L = p.L;
 
-  float pa[NPL], pb[NPL];
+  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
+  float ar[NPL], wh[NPL], wl[NPL];
 #pragma unroll
-  for (int j = 0; j < NPL; ++j) {
-    const int n = j * S + s;
-    pa[j] = 0.f;
-    pb[j] = 0.f;
-    if (cvalid && n < p.NR) {
-      pa[j] = p.Ar[(int64_t)c * p.NR + n] * kLog2e;
-      if (has_imag) pb[j] = p.Ai[(int64_t)c * p.NR + n] * kInv2Pi;
-    } else if (cvalid && n < p.N) {
-      pa[j] = p.Tk[(int64_t)c * p.NT + (n - p.NR)];
-    }
-  }
+  for (int j = 0; j < NPL; ++j)
+    load_gate_params(p.Ar, p.Ai, p.Tk, c, j * S + s, p.N, p.NR, p.NT, cvalid, ar[j], wh[j], wl[j]);
 
   const int nblk = (L + TB - 1) / TB;
   for (int dir = 0; dir < p.ndir; ++dir) {
@@ -105,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
           for (int j = 0; j < NPL; ++j) dst[j * kWave] = h[j];
         }
         const float2 dh = sDH[r][cl];
-        float y = fwd_update<S, NPL>(h, hbp, pa, pb, dh.x, dh.y, &sB[r][s * NPL],
+        float y = fwd_update<S, NPL>(h, hbp, ar, wh, wl, sTab, dh.x, dh.y, &sB[r][s * NPL],
                                      &sC[r][s * NPL], s, p.NR, has_imag);
         y = reduce_states<S>(y);
         if (s == 0 && cvalid) {

@@ -29,7 +29,9 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   const bool cvalid = c < p.D;
   const bool has_imag = p.Ai != nullptr;
 
-  float pa[NPL], pb[NPL], h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
+  __shared__ float2 sTab[16];  // cos, sin of 2 pi k / 16
+  fill_sincos_table(sTab, tid);
+  float ar[NPL], wh[NPL], wl[NPL], h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
   float dt = 0.f, uu = 0.f;
   if (cvalid) {
     dt = p.delta[(int64_t)r * p.dsr + c];
@@ -39,8 +41,6 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int n = j * S + s;
-    pa[j] = 0.f;
-    pb[j] = 0.f;
     h[j] = 0.f;
     hbp[j] = 0.f;
     Bs[j] = 0.f;
@@ -49,21 +49,15 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
       Bs[j] = p.Bc[(int64_t)r * p.bsr + n];
       Cs[j] = p.Cc[(int64_t)r * p.csr + n];
     }
-    if (cvalid && n < p.N) {
-      if (p.h_in != nullptr) {
-        h[j] = p.h_in[sbase + n];
-        hbp[j] = 0.5f * p.beta_in[sbase + n];
-      }
-      if (n < p.NR) {
-        pa[j] = p.Ar[(int64_t)c * p.NR + n] * kLog2e;
-        if (has_imag) pb[j] = p.Ai[(int64_t)c * p.NR + n] * kInv2Pi;
-      } else {
-        pa[j] = p.Tk[(int64_t)c * p.NT + (n - p.NR)];
-      }
+    if (cvalid && n < p.N && p.h_in != nullptr) {
+      h[j] = p.h_in[sbase + n];
+      hbp[j] = 0.5f * p.beta_in[sbase + n];
     }
+    load_gate_params(p.Ar, p.Ai, p.Tk, c, n, p.N, p.NR, p.NT, cvalid, ar[j], wh[j], wl[j]);
   }
+  __syncthreads();  // the sin/cos table
   const float hd = 0.5f * fmul(dt, uu);
-  float y = fwd_update<S, NPL>(h, hbp, pa, pb, dt, hd, Bs, Cs, s, p.NR, has_imag);
+  float y = fwd_update<S, NPL>(h, hbp, ar, wh, wl, sTab, dt, hd, Bs, Cs, s, p.NR, has_imag);
   y = reduce_states<S>(y);
   if (cvalid) {
 #pragma unroll
