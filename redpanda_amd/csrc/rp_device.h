@@ -19,10 +19,9 @@
 // relative drift of the state of ~(steps x bias) and a visible error in the
 // gradients that sum over steps.  The rotational gate is therefore
 // evaluated to ~1 ulp without systematic bias:
-//     exp(dt*Ar)  = 2^(x log2 e), x = fl(dt*Ar) as the reference rounds it,
-//                   the rounding error of x*log2e folded back;
-//     cos / sin   of the angle in revolutions w = dt*(wh + wl), where
-//                   wh + wl = Ai/(2 pi) to 2^-48, reduced exactly to a
+//     exp(dt*Ar)  = 2^(dt (pah + pal)), pah + pal = Ar log2(e) to 2^-48;
+//     cos / sin   of the angle in 1/16 revolutions w = dt (wh + wl), where
+//                   wh + wl = 16 Ai / (2 pi) to 2^-48, reduced exactly to a
 //                   16-entry table and |x| <= pi/16, where short Taylor
 //                   polynomials are accurate to < 1e-9.
 // The forward, the step and the backward's recompute share the code, so the
@@ -38,7 +37,6 @@
 namespace rp {
 
 constexpr float kLog2e = 1.44269504088896340736f;
-constexpr float kLog2eLo = 1.925963e-08f;  // log2(e) - float(log2(e))
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kTwoPi = 6.28318530717958647692f;
 constexpr double kInv2PiD = 0.15915494309189533577;
@@ -89,51 +87,63 @@ __device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
   }
 }
 
-// Per-state gate parameters held in registers: ar = A_real (rotational) or
-// tanh(theta) (tracking; 0 for pad states), wh + wl = A_imag / (2 pi).
+// Per-state gate parameters held in registers.  Rotational states:
+//   pah + pal = A_real * log2(e)      (fp32 pair, |pal| <= ulp(pah)/2)
+//   wh  + wl  = 16 A_imag / (2 pi)    (the angle in 1/16 revolutions),
+//   wlr = wl * pi / 8                 (the low part in radians)
+// so the per-step products dt*pah and dt*wh round once per step, at random,
+// as the reference's fl(dt*A) does, and no constant per-state rounding of
+// log2(e) or 1/(2 pi) biases a gate over time.  Tracking states carry
+// pah = tanh(theta); pad states carry zeros.
 __device__ __forceinline__ void load_gate_params(const float* Ar, const float* Ai, const float* Tk,
                                                  int c, int n, int N, int NR, int NT, bool valid,
-                                                 float& ar, float& wh, float& wl) {
-  ar = 0.f;
+                                                 float& pah, float& pal, float& wh, float& wlr) {
+  pah = 0.f;
+  pal = 0.f;
   wh = 0.f;
-  wl = 0.f;
+  wlr = 0.f;
   if (!valid) return;
   if (n < NR) {
-    ar = Ar[(int64_t)c * NR + n];
+    const double P = (double)Ar[(int64_t)c * NR + n] * 1.4426950408889634074;
+    pah = (float)P;
+    pal = (float)(P - (double)pah);
     if (Ai != nullptr) {
-      const double w = (double)Ai[(int64_t)c * NR + n] * kInv2PiD;
-      wh = (float)w;
-      wl = (float)(w - (double)wh);
+      const double W = (double)Ai[(int64_t)c * NR + n] * (16.0 * kInv2PiD);
+      wh = (float)W;
+      wlr = (float)((W - (double)wh) * 0.39269908169872415481);  // * pi / 8
     }
   } else if (n < N) {
-    ar = Tk[(int64_t)c * NT + (n - NR)];
+    pah = Tk[(int64_t)c * NT + (n - NR)];
   }
 }
 
-// Rotational gate g = exp(dt*ar) cos(2 pi dt (wh + wl)); with WITH_SIN also
-// es = exp(dt*ar) sin(...) for the backward.  The cos path is the same code
-// in both instantiations, so g is bitwise the same.
+constexpr float kPi8 = 0.39269908169872415481f;  // pi / 8: radians per table step
+constexpr float kRint = 12582912.f;               // 1.5 * 2^23: x + kRint rounds x to an integer
+
+// Rotational gate g = 2^(dt (pah + pal)) cos(pi/8 dt (wh + wl)); with WITH_SIN
+// also es = 2^(...) sin(...) for the backward.  The angle is reduced exactly
+// to k + rr (k an integer, |rr| <= 1/2, in 1/16 revolutions) by the
+// round-to-integer addition; cos / sin of the 16 table angles come from LDS
+// and those of the remainder (|x| <= pi/16) from Taylor polynomials whose
+// truncation error is below 1e-9.  The cos path is the same code in both
+// instantiations, so g is bitwise the same.
 template <bool WITH_SIN>
-__device__ __forceinline__ float rot_gate(float dt, float ar, float wh, float wl, bool has_imag,
-                                          const float2* tab, float& es) {
-  const float x = fmul(dt, ar);
-  const float p = fmul(x, kLog2e);
-  const float perr = ffma(x, kLog2eLo, ffma(x, kLog2e, -p));
-  const float e0 = exp2_hw(p);
-  const float e = ffma(e0, fmul(perr, kLn2), e0);
+__device__ __forceinline__ float rot_gate(float dt, float pah, float pal, float wh, float wlr,
+                                          bool has_imag, const float2* tab, float& es) {
+  const float e = exp2_hw(ffma(dt, pal, fmul(dt, pah)));
   if (!has_imag) {
     es = 0.f;
     return e;
   }
   const float w = fmul(dt, wh);
-  const float wlo = ffma(dt, wl, ffma(dt, wh, -w));
-  const float kf = __builtin_rintf(fmul(w, 16.f));
-  const float rr = ffma(kf, -0.0625f, w) + wlo;  // exact reduction, |rr| <= 1/32
-  const float xr = fmul(rr, kTwoPi);
+  const float t = w + kRint;
+  const float kf = t - kRint;                    // rint(w), exact
+  const float rr = w - kf;                       // exact
+  const float xr = ffma(rr, kPi8, fmul(dt, wlr));
   const float x2 = fmul(xr, xr);
   const float cm1 = fmul(x2, ffma(x2, ffma(x2, -1.f / 720.f, 1.f / 24.f), -0.5f));  // cos - 1
   const float sx = ffma(fmul(xr, x2), ffma(x2, 1.f / 120.f, -1.f / 6.f), xr);        // sin
-  const float2 cs = tab[(int)kf & 15];
+  const float2 cs = tab[__float_as_int(t) & 15];
   const float cv = ffma(-cs.y, sx, ffma(cs.x, cm1, cs.x));
   if (WITH_SIN) {
     const float sv = ffma(cs.x, sx, ffma(cs.y, cm1, cs.y));
@@ -145,18 +155,35 @@ __device__ __forceinline__ float rot_gate(float dt, float ar, float wh, float wl
 }
 
 // Gate of state j for lane slice s: rotational if n < NR, else the tracking
-// gate ar = tanh(theta) (pad states beyond N carry ar = 0 and B = C = 0).
+// gate pah = tanh(theta) (pad states beyond N carry 0 and B = C = 0).
 template <int S, bool WITH_SIN>
-__device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float ar,
-                                         float wh, float wl, const float2* tab, float& es) {
+__device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pah,
+                                         float pal, float wh, float wlr, const float2* tab,
+                                         float& es) {
   if (j * S >= NR) {
     es = 0.f;
-    return ar;
+    return pah;
   }
-  const float gr = rot_gate<WITH_SIN>(dt, ar, wh, wl, has_imag, tab, es);
+  const float gr = rot_gate<WITH_SIN>(dt, pah, pal, wh, wlr, has_imag, tab, es);
   if ((j + 1) * S <= NR || j * S + s < NR) return gr;
   es = 0.f;
-  return ar;
+  return pah;
+}
+
+// Per-lane gate parameters of NPL states.
+template <int NPL>
+struct GateRegs {
+  float pah[NPL], pal[NPL], wh[NPL], wlr[NPL];
+};
+
+template <int S, int NPL>
+__device__ __forceinline__ void load_gate_regs(GateRegs<NPL>& gp, const float* Ar, const float* Ai,
+                                               const float* Tk, int c, int s, int N, int NR,
+                                               int NT, bool valid) {
+#pragma unroll
+  for (int j = 0; j < NPL; ++j)
+    load_gate_params(Ar, Ai, Tk, c, j * S + s, N, NR, NT, valid, gp.pah[j], gp.pal[j], gp.wh[j],
+                     gp.wlr[j]);
 }
 
 // One recurrence step for the lane's NPL states; returns the lane's partial
@@ -165,8 +192,7 @@ __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, fl
 // previous step's hb.  Shared verbatim by the scan and step kernels.
 template <int S, int NPL>
 __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
-                                            const float (&ar)[NPL], const float (&wh)[NPL],
-                                            const float (&wl)[NPL], const float2* tab, float dt,
+                                            const GateRegs<NPL>& gp, const float2* tab, float dt,
                                             float hdu, const float* __restrict__ Bs,
                                             const float* __restrict__ Cs, int s, int NR,
                                             bool has_imag) {
@@ -174,7 +200,8 @@ __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     float unused;
-    const float g = gate_of<S, false>(j, s, NR, has_imag, dt, ar[j], wh[j], wl[j], tab, unused);
+    const float g = gate_of<S, false>(j, s, NR, has_imag, dt, gp.pah[j], gp.pal[j], gp.wh[j],
+                                      gp.wlr[j], tab, unused);
     const float hb = fmul(hdu, Bs[j]);
     const float sm = h[j] + hbp[j];
     h[j] = ffma(g, sm, hb);

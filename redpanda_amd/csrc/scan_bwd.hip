@@ -63,12 +63,11 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
   const int L = p.L;
 
   fill_sincos_table(sTab, tid);  // first read after the staging barrier below
-  // ar: A_real (rotational) or tanh(theta) (tracking); wh + wl: A_imag/(2 pi)
-  float ar[NPL], wh[NPL], wl[NPL];
+  GateRegs<NPL> gp;
+  load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
   double dpa[NPL], dpb[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    load_gate_params(p.Ar, p.Ai, p.Tk, c, j * S + s, p.N, p.NR, p.NT, cvalid, ar[j], wh[j], wl[j]);
     dpa[j] = 0.0;
     dpb[j] = 0.0;
   }
@@ -171,8 +170,8 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
                 float es;
-                const float g = gate_of<S, true>(j, s, p.NR, has_imag, dt, ar[j], wh[j], wl[j],
-                                                 sTab, es);
+                const float g = gate_of<S, true>(j, s, p.NR, has_imag, dt, gp.pah[j], gp.pal[j],
+                                                 gp.wh[j], gp.wlr[j], sTab, es);
                 const float hb = fmul(hd, sB[row][s * NPL + j]);
                 const float sm = hc[j] + hbp[j];
                 SP[m][j] = sm;
@@ -217,8 +216,8 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
                   const float t2 = fmul(dg, ES[m][j]);
                   cpa[j] = ffma(t1, dt, cpa[j]);
                   cpb[j] = ffma(t2, dt, cpb[j]);
-                  ddA = ffma(ar[j], t1, ddA);
-                  ddB = ffma(wh[j], t2, ddB);
+                  ddA = ffma(gp.pah[j], t1, ddA);  // Ar log2(e) dg g
+                  ddB = ffma(gp.wh[j], t2, ddB);   // Ai 16/(2 pi) dg e sin
                 } else {
                   cpa[j] = cpa[j] + dg;
                 }
@@ -235,7 +234,7 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
               ddB = reduce_states<S>(ddB);
               sBc = reduce_states<S>(sBc);
               if (s == 0) {
-                const float ddt = (ddA - fmul(kTwoPi, ddB)) + fmul(0.5f * uu, sBc);
+                const float ddt = ffma(kLn2, ddA, -fmul(kPi8, ddB)) + fmul(0.5f * uu, sBc);
                 const float dut = fmul(0.5f * dt, sBc);
                 sDD[m0 + m][cl] = make_float2(ddt, dut);
               }

@@ -38,10 +38,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   const int L = p.L;
 
   fill_sincos_table(sTab, tid);  // first read after the staging barrier below
-  float ar[NPL], wh[NPL], wl[NPL];
-#pragma unroll
-  for (int j = 0; j < NPL; ++j)
-    load_gate_params(p.Ar, p.Ai, p.Tk, c, j * S + s, p.N, p.NR, p.NT, cvalid, ar[j], wh[j], wl[j]);
+  GateRegs<NPL> gp;
+  load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
 
   const int nblk = (L + TB - 1) / TB;
   for (int dir = 0; dir < p.ndir; ++dir) {
@@ -98,7 +96,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
           for (int j = 0; j < NPL; ++j) dst[j * kWave] = h[j];
         }
         const float2 dh = sDH[r][cl];
-        float y = fwd_update<S, NPL>(h, hbp, ar, wh, wl, sTab, dh.x, dh.y, &sB[r][s * NPL],
+        float y = fwd_update<S, NPL>(h, hbp, gp, sTab, dh.x, dh.y, &sB[r][s * NPL],
                                      &sC[r][s * NPL], s, p.NR, has_imag);
         y = reduce_states<S>(y);
         if (s == 0 && cvalid) {

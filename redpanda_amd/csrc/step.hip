@@ -31,7 +31,8 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
 
   __shared__ float2 sTab[16];  // cos, sin of 2 pi k / 16
   fill_sincos_table(sTab, tid);
-  float ar[NPL], wh[NPL], wl[NPL], h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
+  GateRegs<NPL> gp;
+  float h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
   float dt = 0.f, uu = 0.f;
   if (cvalid) {
     dt = p.delta[(int64_t)r * p.dsr + c];
@@ -53,11 +54,11 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
       h[j] = p.h_in[sbase + n];
       hbp[j] = 0.5f * p.beta_in[sbase + n];
     }
-    load_gate_params(p.Ar, p.Ai, p.Tk, c, n, p.N, p.NR, p.NT, cvalid, ar[j], wh[j], wl[j]);
   }
+  load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
   __syncthreads();  // the sin/cos table
   const float hd = 0.5f * fmul(dt, uu);
-  float y = fwd_update<S, NPL>(h, hbp, ar, wh, wl, sTab, dt, hd, Bs, Cs, s, p.NR, has_imag);
+  float y = fwd_update<S, NPL>(h, hbp, gp, sTab, dt, hd, Bs, Cs, s, p.NR, has_imag);
   y = reduce_states<S>(y);
   if (cvalid) {
 #pragma unroll
