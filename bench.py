@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--no-step", action="store_true", help="skip the step() workload")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run one plain 1 GiB device copy (reads 1 GiB, writes 1 GiB): "
+                         "the reference dispatch that scales FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -380,6 +383,14 @@ def main():
                          "avg_launch_s": step["t_launch"]},
         }
     line["cpu_baseline"] = cpu
+    if args.calib_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: {src.numel() * 4} bytes read and written",
+              file=sys.stderr, flush=True)
+        del src, dst
     print(json.dumps(line), flush=True)
 
 

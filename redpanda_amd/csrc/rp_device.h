@@ -12,18 +12,17 @@
 // the step kernel uses the very same functions, so step == scan bit for bit.
 //
 // Gate arithmetic (rot_gate below).  exp uses the transcendental unit
-// (v_exp_f32 is good to 0.8 ulp and unbiased); cos / sin do not: measured on
-// gfx950, v_cos_f32 / v_sin_f32 are off by up to ~2 ulp with a bias of
-// +-0.3..0.6 ulp that depends on the angle (-0.6 ulp near cos = 1).  A gate
-// close to 1 carries state over tens of steps, so a biased gate turns into a
-// relative drift of the state of ~(steps x bias) and a visible error in the
-// gradients that sum over steps.  The rotational gate is therefore
-// evaluated to ~1 ulp without systematic bias:
-//     exp(dt*Ar)  = 2^(dt (pah + pal)), pah + pal = Ar log2(e) to 2^-48;
-//     cos / sin   of the angle in 1/16 revolutions w = dt (wh + wl), where
-//                   wh + wl = 16 Ai / (2 pi) to 2^-48, reduced exactly to a
-//                   16-entry table and |x| <= pi/16, where short Taylor
-//                   polynomials are accurate to < 1e-9.
+// (v_exp_f32: 0.8 ulp, unbiased); cos / sin do not: measured on gfx950,
+// v_cos_f32 / v_sin_f32 are off by up to ~2 ulp with a bias of +-0.3..0.6 ulp
+// that depends on the angle (-0.6 ulp near cos = 1).  That bias is a fixed
+// relative error per step, so a gate close to 1, which carries state over
+// M ~ 1/(1-g) steps, turns it into a relative drift of ~M x bias in the state
+// and in every gradient that sums over steps.  The rotational cos / sin are
+// therefore evaluated to ~1 ulp without bias: the angle in 1/16 revolutions
+// is reduced exactly to a table index plus a remainder |x| <= pi/16, where
+// short Taylor polynomials are accurate to < 3e-9.  (Rounding Ar*log2(e)
+// and 16*Ai/(2 pi) once per state is harmless by contrast: its error
+// scales with dt*A, so it stays ~1 ulp of the state over any memory length.)
 // The forward, the step and the backward's recompute share the code, so the
 // backward recomputes exactly the gates the forward used.
 #pragma once
@@ -87,31 +86,18 @@ __device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
   }
 }
 
-// Per-state gate parameters held in registers.  Rotational states:
-//   pah + pal = A_real * log2(e)      (fp32 pair, |pal| <= ulp(pah)/2)
-//   wh  + wl  = 16 A_imag / (2 pi)    (the angle in 1/16 revolutions),
-//   wlr = wl * pi / 8                 (the low part in radians)
-// so the per-step products dt*pah and dt*wh round once per step, at random,
-// as the reference's fl(dt*A) does, and no constant per-state rounding of
-// log2(e) or 1/(2 pi) biases a gate over time.  Tracking states carry
-// pah = tanh(theta); pad states carry zeros.
+// Per-state gate parameters held in registers: pah = fl(A_real log2(e)) and
+// wh = fl(16 A_imag / (2 pi)) (the angle rate in 1/16 revolutions) for
+// rotational states; pah = tanh(theta) for tracking states; zeros for pad.
 __device__ __forceinline__ void load_gate_params(const float* Ar, const float* Ai, const float* Tk,
                                                  int c, int n, int N, int NR, int NT, bool valid,
-                                                 float& pah, float& pal, float& wh, float& wlr) {
+                                                 float& pah, float& wh) {
   pah = 0.f;
-  pal = 0.f;
   wh = 0.f;
-  wlr = 0.f;
   if (!valid) return;
   if (n < NR) {
-    const double P = (double)Ar[(int64_t)c * NR + n] * 1.4426950408889634074;
-    pah = (float)P;
-    pal = (float)(P - (double)pah);
-    if (Ai != nullptr) {
-      const double W = (double)Ai[(int64_t)c * NR + n] * (16.0 * kInv2PiD);
-      wh = (float)W;
-      wlr = (float)((W - (double)wh) * 0.39269908169872415481);  // * pi / 8
-    }
+    pah = (float)((double)Ar[(int64_t)c * NR + n] * 1.4426950408889634074);
+    if (Ai != nullptr) wh = (float)((double)Ai[(int64_t)c * NR + n] * (16.0 * kInv2PiD));
   } else if (n < N) {
     pah = Tk[(int64_t)c * NT + (n - NR)];
   }
@@ -119,30 +105,46 @@ __device__ __forceinline__ void load_gate_params(const float* Ar, const float* A
 
 constexpr float kPi8 = 0.39269908169872415481f;  // pi / 8: radians per table step
 constexpr float kRint = 12582912.f;               // 1.5 * 2^23: x + kRint rounds x to an integer
+// cos(pi/8 r) - 1 = r^2 (kC2 + r^2 (kC4 + r^2 kC6)),  sin(pi/8 r) = r (kS1 + r^2 (kS3 + r^2 kS5))
+// for |r| <= 1/2 (Taylor, truncation < 6e-11 and < 3e-9)
+constexpr float kC2 = -0.07710628438351061f, kC4 = 0.0009908965152384687f,
+                kC6 = -5.093623233240468e-06f;
+constexpr float kS1 = 0.39269908169872414f, kS3 = -0.010093189023535096f,
+                kS5 = 7.78248303185225e-05f;
 
-// Rotational gate g = 2^(dt (pah + pal)) cos(pi/8 dt (wh + wl)); with WITH_SIN
-// also es = 2^(...) sin(...) for the backward.  The angle is reduced exactly
-// to k + rr (k an integer, |rr| <= 1/2, in 1/16 revolutions) by the
-// round-to-integer addition; cos / sin of the 16 table angles come from LDS
-// and those of the remainder (|x| <= pi/16) from Taylor polynomials whose
-// truncation error is below 1e-9.  The cos path is the same code in both
-// instantiations, so g is bitwise the same.
+// How a kernel instantiation knows the rotational / tracking split:
+//   RJ   leading state slots j < RJ are rotational in every lane (compile
+//        time); slots j >= RJ are decided at run time from NR;
+//   IMAG 1: complex rotational gates, 0: real decay gates, 2: decided at
+//        run time from has_imag.
+// Specialised and generic instantiations run the same arithmetic, so their
+// results are bitwise equal.
+template <int RJ, int IMAG>
+struct GateKind {
+  static constexpr int kRJ = RJ;
+  static constexpr int kImag = IMAG;
+};
+
+// Rotational gate g = 2^(dt pah) cos(pi/8 dt wh); with WITH_SIN also
+// es = 2^(dt pah) sin(pi/8 dt wh) for the backward.  The angle dt*wh is split
+// exactly into an integer k (the table index, by the round-to-integer
+// addition) and a remainder |r| <= 1/2.  The cos path is the same code in
+// both instantiations, so g is bitwise the same.
 template <bool WITH_SIN>
-__device__ __forceinline__ float rot_gate(float dt, float pah, float pal, float wh, float wlr,
-                                          bool has_imag, const float2* tab, float& es) {
-  const float e = exp2_hw(ffma(dt, pal, fmul(dt, pah)));
-  if (!has_imag) {
+__device__ __forceinline__ float rot_gate(float dt, float pah, float wh, bool imag,
+                                          const float2* tab, float& es) {
+  const float e = exp2_hw(fmul(dt, pah));
+  if (!imag) {
     es = 0.f;
     return e;
   }
   const float w = fmul(dt, wh);
   const float t = w + kRint;
   const float kf = t - kRint;                    // rint(w), exact
-  const float rr = w - kf;                       // exact
-  const float xr = ffma(rr, kPi8, fmul(dt, wlr));
-  const float x2 = fmul(xr, xr);
-  const float cm1 = fmul(x2, ffma(x2, ffma(x2, -1.f / 720.f, 1.f / 24.f), -0.5f));  // cos - 1
-  const float sx = ffma(fmul(xr, x2), ffma(x2, 1.f / 120.f, -1.f / 6.f), xr);        // sin
+  const float r = w - kf;                        // exact
+  const float r2 = fmul(r, r);
+  const float cm1 = fmul(r2, ffma(r2, ffma(r2, kC6, kC4), kC2));  // cos - 1
+  const float sx = fmul(r, ffma(r2, ffma(r2, kS5, kS3), kS1));    // sin
   const float2 cs = tab[__float_as_int(t) & 15];
   const float cv = ffma(-cs.y, sx, ffma(cs.x, cm1, cs.x));
   if (WITH_SIN) {
@@ -154,17 +156,30 @@ __device__ __forceinline__ float rot_gate(float dt, float pah, float pal, float 
   return fmul(e, cv);
 }
 
-// Gate of state j for lane slice s: rotational if n < NR, else the tracking
-// gate pah = tanh(theta) (pad states beyond N carry 0 and B = C = 0).
-template <int S, bool WITH_SIN>
+// Whether state slot j of lane slice s is rotational (n = j*S + s < NR).
+template <int S, class GK>
+__device__ __forceinline__ bool is_rot(int j, int s, int NR) {
+  if (j < GK::kRJ) return true;
+  if (j * S >= NR) return false;
+  return (j + 1) * S <= NR || j * S + s < NR;
+}
+
+template <class GK>
+__device__ __forceinline__ bool imag_of(bool has_imag) {
+  return GK::kImag == 2 ? has_imag : GK::kImag == 1;
+}
+
+// Gate of state slot j for lane slice s: rotational if n < NR, else the
+// tracking gate pah = tanh(theta) (pad states beyond N carry 0 and B = C = 0).
+template <int S, class GK, bool WITH_SIN>
 __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pah,
-                                         float pal, float wh, float wlr, const float2* tab,
-                                         float& es) {
+                                         float wh, const float2* tab, float& es) {
+  if (j < GK::kRJ) return rot_gate<WITH_SIN>(dt, pah, wh, imag_of<GK>(has_imag), tab, es);
   if (j * S >= NR) {
     es = 0.f;
     return pah;
   }
-  const float gr = rot_gate<WITH_SIN>(dt, pah, pal, wh, wlr, has_imag, tab, es);
+  const float gr = rot_gate<WITH_SIN>(dt, pah, wh, imag_of<GK>(has_imag), tab, es);
   if ((j + 1) * S <= NR || j * S + s < NR) return gr;
   es = 0.f;
   return pah;
@@ -173,7 +188,7 @@ __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, fl
 // Per-lane gate parameters of NPL states.
 template <int NPL>
 struct GateRegs {
-  float pah[NPL], pal[NPL], wh[NPL], wlr[NPL];
+  float pah[NPL], wh[NPL];
 };
 
 template <int S, int NPL>
@@ -182,15 +197,14 @@ __device__ __forceinline__ void load_gate_regs(GateRegs<NPL>& gp, const float* A
                                                int NT, bool valid) {
 #pragma unroll
   for (int j = 0; j < NPL; ++j)
-    load_gate_params(Ar, Ai, Tk, c, j * S + s, N, NR, NT, valid, gp.pah[j], gp.pal[j], gp.wh[j],
-                     gp.wlr[j]);
+    load_gate_params(Ar, Ai, Tk, c, j * S + s, N, NR, NT, valid, gp.pah[j], gp.wh[j]);
 }
 
 // One recurrence step for the lane's NPL states; returns the lane's partial
 //     y = sum_j h_j C_j     (FMA chain in j order).
 // hdu = (dt*u)/2, so hb = hdu*B_n equals beta_t/2 exactly; hbp holds the
 // previous step's hb.  Shared verbatim by the scan and step kernels.
-template <int S, int NPL>
+template <int S, int NPL, class GK>
 __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
                                             const GateRegs<NPL>& gp, const float2* tab, float dt,
                                             float hdu, const float* __restrict__ Bs,
@@ -200,8 +214,7 @@ __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     float unused;
-    const float g = gate_of<S, false>(j, s, NR, has_imag, dt, gp.pah[j], gp.pal[j], gp.wh[j],
-                                      gp.wlr[j], tab, unused);
+    const float g = gate_of<S, GK, false>(j, s, NR, has_imag, dt, gp.pah[j], gp.wh[j], tab, unused);
     const float hb = fmul(hdu, Bs[j]);
     const float sm = h[j] + hbp[j];
     h[j] = ffma(g, sm, hb);

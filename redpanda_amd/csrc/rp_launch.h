@@ -14,7 +14,7 @@ constexpr int kThreads = kWave * kWaves;
 // and the checkpoint interval of the backward's recompute.
 constexpr int kFwdTB = 32;
 constexpr int kBwdTB = 16;
-constexpr int kCkptK = 8;
+constexpr int kCkptK = 4;
 
 struct ScanParams {
   const void* delta;
@@ -82,11 +82,17 @@ struct StepParams {
 // states each.  Returns false when N is beyond the compiled shapes.
 bool choose_shape(int N, int* S, int* NPL);
 
-hipError_t launch_scan_fwd(int S, int NPL, const ScanParams& p, const FwdOut& o, hipStream_t st);
-hipError_t launch_scan_bwd(int S, int NPL, const ScanParams& p, const BwdIO& io, hipStream_t st);
+// `spec`: every state slot j < NPL-1 is rotational in every lane (NR >=
+// S*(NPL-1)) and the gates are complex; selects the instantiation that
+// resolves the rotational / tracking split at compile time (bitwise the
+// same results as the generic one).
+hipError_t launch_scan_fwd(int S, int NPL, bool spec, const ScanParams& p, const FwdOut& o,
+                           hipStream_t st);
+hipError_t launch_scan_bwd(int S, int NPL, bool spec, const ScanParams& p, const BwdIO& io,
+                           hipStream_t st);
 hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
                                float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st);
-hipError_t launch_step(int S, int NPL, const StepParams& p, hipStream_t st);
+hipError_t launch_step(int S, int NPL, bool spec, const StepParams& p, hipStream_t st);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 
 }  // namespace rp

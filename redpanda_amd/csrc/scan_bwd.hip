@@ -29,13 +29,15 @@
 //   * parameter gradients (dA, dTk): 8-step fp32 chunk sums accumulated in
 //     float64 per lane over the batch group, then float64 across groups.
 
+#include <type_traits>
+
 #include "rp_device.h"
 #include "rp_launch.h"
 
 namespace rp {
 
-template <int S, int NPL>
-__global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, BwdIO io) {
+template <int S, int NPL, class GK>
+__global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
   using Sh = Shape<S, NPL>;
   constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = kBwdTB, K = kCkptK;
   constexpr int KR = NP <= 40 ? K : K / 2;  // steps per channel-sum fold
@@ -159,118 +161,125 @@ __global__ __launch_bounds__(kThreads, 2) void scan_bwd_kernel(ScanParams p, Bwd
               hbp[j] = fmul(hdp, sB[m0][s * NPL + j]);
             }
           }
-          // recompute the chunk: s_{t-1}, g_t and e*sin for every step
-          float SP[K][NPL], G[K][NPL], ES[K][NPL];
+          // The chunk body, instantiated twice: FULL (all K steps present, the
+          // common case; straight-line code) and a guarded tail for a last
+          // chunk shorter than K.
+          auto chunk_body = [&](auto full_tag) {
+            constexpr bool FULL = decltype(full_tag)::value;
+            // recompute the chunk: s_{t-1}, g_t and e*sin for every step
+            float SP[K][NPL], G[K][NPL], ES[K][NPL];
 #pragma unroll
-          for (int m = 0; m < K; ++m) {
-            if (m < kcnt) {
-              const int row = m0 + m + 1;
-              const float dt = sCh[row][cl].x;
-              const float hd = sCh[row][cl].y;
+            for (int m = 0; m < K; ++m) {
+              if (FULL || m < kcnt) {
+                const int row = m0 + m + 1;
+                const float dt = sCh[row][cl].x;
+                const float hd = sCh[row][cl].y;
 #pragma unroll
-              for (int j = 0; j < NPL; ++j) {
-                float es;
-                const float g = gate_of<S, true>(j, s, p.NR, has_imag, dt, gp.pah[j], gp.pal[j],
-                                                 gp.wh[j], gp.wlr[j], sTab, es);
-                const float hb = fmul(hd, sB[row][s * NPL + j]);
-                const float sm = hc[j] + hbp[j];
-                SP[m][j] = sm;
-                G[m][j] = g;
-                ES[m][j] = es;
-                hc[j] = ffma(g, sm, hb);
-                hbp[j] = hb;
-              }
-            }
-          }
-          // adjoint over the chunk, last step first.  Parameter gradients sum
-          // into chunk-local fp32 accumulators, then into float64.
-          float cpa[NPL], cpb[NPL];
-#pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            cpa[j] = 0.f;
-            cpb[j] = 0.f;
-          }
-#pragma unroll
-          for (int m = K - 1; m >= 0; --m) {
-            if (m < kcnt) {
-              const int row = m0 + m + 1;
-              const float4 ch = sCh[row][cl];
-              const float dt = ch.x, hd = ch.y, uu = ch.z, dy = ch.w;
-              float ddA = 0.f, ddB = 0.f, sBc = 0.f;
-#pragma unroll
-              for (int j = 0; j < NPL; ++j) {
-                const float Bv = sB[row][s * NPL + j];
-                const float Cv = sC[row][s * NPL + j];
-                const bool all_rot = (j + 1) * S <= p.NR;
-                const bool all_trk = j * S >= p.NR;
-                const bool rot = all_rot || (!all_trk && (j * S + s < p.NR));
-                const float g = G[m][j];
-                const float hb = fmul(hd, Bv);
-                const float ht = ffma(g, SP[m][j], hb);
-                const float q = ffma(dy, Cv, gq[j]);
-                const float dhb = q + gr[j];
-                sBc = ffma(dhb, Bv, sBc);
-                const float dg = fmul(q, SP[m][j]);
-                if (rot) {
-                  const float t1 = fmul(dg, g);
-                  const float t2 = fmul(dg, ES[m][j]);
-                  cpa[j] = ffma(t1, dt, cpa[j]);
-                  cpb[j] = ffma(t2, dt, cpb[j]);
-                  ddA = ffma(gp.pah[j], t1, ddA);  // Ar log2(e) dg g
-                  ddB = ffma(gp.wh[j], t2, ddB);   // Ai 16/(2 pi) dg e sin
-                } else {
-                  cpa[j] = cpa[j] + dg;
-                }
-                gq[j] = fmul(g, q);
-                gr[j] = gq[j];
-                const float xB = reduce_row<S>(fmul(dhb, hd));
-                const float xC = reduce_row<S>(fmul(dy, ht));
-                if (row_leader) {
-                  sRed[m % KR][0][wrow][s * NPL + j] = xB;
-                  sRed[m % KR][1][wrow][s * NPL + j] = xC;
+                for (int j = 0; j < NPL; ++j) {
+                  float es;
+                  const float g = gate_of<S, GK, true>(j, s, p.NR, has_imag, dt, gp.pah[j],
+                                                       gp.wh[j], sTab, es);
+                  const float hb = fmul(hd, sB[row][s * NPL + j]);
+                  const float sm = hc[j] + hbp[j];
+                  SP[m][j] = sm;
+                  G[m][j] = g;
+                  ES[m][j] = es;
+                  hc[j] = ffma(g, sm, hb);
+                  hbp[j] = hb;
                 }
               }
-              ddA = reduce_states<S>(ddA);
-              ddB = reduce_states<S>(ddB);
-              sBc = reduce_states<S>(sBc);
-              if (s == 0) {
-                const float ddt = ffma(kLn2, ddA, -fmul(kPi8, ddB)) + fmul(0.5f * uu, sBc);
-                const float dut = fmul(0.5f * dt, sBc);
-                sDD[m0 + m][cl] = make_float2(ddt, dut);
-              }
             }
-            if (m % KR == 0) {
-              // fold the 16 row partials of steps [m, m + KR) into this
-              // tile's global dB / dC partials
-              __syncthreads();
-              for (int e = tid; e < KR * 2 * p.N; e += kThreads) {
-                const int rr = e / (2 * p.N);
-                const int rem = e % (2 * p.N);
-                const int which = rem / p.N, n = rem % p.N;
-                if (m + rr < kcnt) {
-                  const int k = (n % S) * NPL + n / S;
-                  float v = sRed[rr][which][0][k];
+            // adjoint over the chunk, last step first.  Parameter gradients
+            // sum into chunk-local fp32 accumulators, then into float64.
+            float cpa[NPL], cpb[NPL];
 #pragma unroll
-                  for (int w = 1; w < NRW; ++w) v = v + sRed[rr][which][w][k];
-                  const int i = i0 + m0 + m + rr;
-                  const int t = dir ? (L - 1 - i) : i;
-                  float* dst = io.part_bc +
-                               (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
-                               (int64_t)t * p.N + n;
-                  if (dir == 0)
-                    *dst = v;
-                  else
-                    *dst = *dst + v;
+            for (int j = 0; j < NPL; ++j) {
+              cpa[j] = 0.f;
+              cpb[j] = 0.f;
+            }
+#pragma unroll
+            for (int m = K - 1; m >= 0; --m) {
+              if (FULL || m < kcnt) {
+                const int row = m0 + m + 1;
+                const float4 ch = sCh[row][cl];
+                const float dt = ch.x, hd = ch.y, uu = ch.z, dy = ch.w;
+                float ddA = 0.f, ddB = 0.f, sBc = 0.f;
+#pragma unroll
+                for (int j = 0; j < NPL; ++j) {
+                  const float Bv = sB[row][s * NPL + j];
+                  const float Cv = sC[row][s * NPL + j];
+                  const float g = G[m][j];
+                  const float hb = fmul(hd, Bv);
+                  const float ht = ffma(g, SP[m][j], hb);
+                  const float q = ffma(dy, Cv, gq[j]);
+                  const float dhb = q + gr[j];
+                  sBc = ffma(dhb, Bv, sBc);
+                  const float dg = fmul(q, SP[m][j]);
+                  if (is_rot<S, GK>(j, s, p.NR)) {
+                    const float t1 = fmul(dg, g);
+                    const float t2 = fmul(dg, ES[m][j]);
+                    cpa[j] = ffma(t1, dt, cpa[j]);
+                    cpb[j] = ffma(t2, dt, cpb[j]);
+                    ddA = ffma(gp.pah[j], t1, ddA);  // Ar log2(e) dg g
+                    ddB = ffma(gp.wh[j], t2, ddB);   // Ai 16/(2 pi) dg e sin
+                  } else {
+                    cpa[j] = cpa[j] + dg;
+                  }
+                  gq[j] = fmul(g, q);
+                  gr[j] = gq[j];
+                  const float xB = reduce_row<S>(fmul(dhb, hd));
+                  const float xC = reduce_row<S>(fmul(dy, ht));
+                  if (row_leader) {
+                    sRed[m % KR][0][wrow][s * NPL + j] = xB;
+                    sRed[m % KR][1][wrow][s * NPL + j] = xC;
+                  }
+                }
+                ddA = reduce_states<S>(ddA);
+                ddB = reduce_states<S>(ddB);
+                sBc = reduce_states<S>(sBc);
+                if (s == 0) {
+                  const float ddt = ffma(kLn2, ddA, -fmul(kPi8, ddB)) + fmul(0.5f * uu, sBc);
+                  const float dut = fmul(0.5f * dt, sBc);
+                  sDD[m0 + m][cl] = make_float2(ddt, dut);
                 }
               }
-              __syncthreads();
-            }
-          }
+              if (m % KR == 0) {
+                // fold the 16 row partials of steps [m, m + KR) into this
+                // tile's global dB / dC partials
+                __syncthreads();
+                for (int e = tid; e < KR * 2 * p.N; e += kThreads) {
+                  const int rr = e / (2 * p.N);
+                  const int rem = e % (2 * p.N);
+                  const int which = rem / p.N, n = rem % p.N;
+                  if (m + rr < kcnt) {
+                    const int k = (n % S) * NPL + n / S;
+                    float v = sRed[rr][which][0][k];
 #pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            dpa[j] += (double)cpa[j];
-            dpb[j] += (double)cpb[j];
-          }
+                    for (int w = 1; w < NRW; ++w) v = v + sRed[rr][which][w][k];
+                    const int i = i0 + m0 + m + rr;
+                    const int t = dir ? (L - 1 - i) : i;
+                    float* dst = io.part_bc +
+                                 (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
+                                 (int64_t)t * p.N + n;
+                    if (dir == 0)
+                      *dst = v;
+                    else
+                      *dst = *dst + v;
+                  }
+                }
+                __syncthreads();
+              }
+            }
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) {
+              dpa[j] += (double)cpa[j];
+              dpb[j] += (double)cpb[j];
+            }
+          };
+          if (kcnt == K)
+            chunk_body(std::true_type{});
+          else
+            chunk_body(std::false_type{});
         }
         // the block's (d_delta, d_u) rows, written channel-contiguous
         for (int e = tid; e < cnt * CB; e += kThreads) {
@@ -353,16 +362,19 @@ __global__ void bwd_reduce_par(const double* __restrict__ part, float* __restric
   }
 }
 
-template <int S, int NPL>
+template <int S, int NPL, class GK>
 static hipError_t launch_bwd_t(const ScanParams& p, const BwdIO& io, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ntiles * io.nbg));
-  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL>), grid, dim3(kThreads), 0, st, p, io);
+  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK>), grid, dim3(kThreads), 0, st, p, io);
   return hipGetLastError();
 }
 
-hipError_t launch_scan_bwd(int S, int NPL, const ScanParams& p, const BwdIO& io, hipStream_t st) {
-#define RP_CASE(SS, NN) \
-  if (S == SS && NPL == NN) return launch_bwd_t<SS, NN>(p, io, st);
+hipError_t launch_scan_bwd(int S, int NPL, bool spec, const ScanParams& p, const BwdIO& io,
+                           hipStream_t st) {
+#define RP_CASE(SS, NN)                                                          \
+  if (S == SS && NN == NPL)                                                      \
+    return spec ? launch_bwd_t<SS, NN, GateKind<NN - 1, 1>>(p, io, st)           \
+                : launch_bwd_t<SS, NN, GateKind<0, 2>>(p, io, st);
   RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
   return hipErrorInvalidValue;

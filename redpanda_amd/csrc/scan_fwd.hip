@@ -18,7 +18,7 @@
 
 namespace rp {
 
-template <int S, int NPL>
+template <int S, int NPL, class GK>
 __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut o) {
   using Sh = Shape<S, NPL>;
   constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = kFwdTB;
@@ -96,8 +96,8 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
           for (int j = 0; j < NPL; ++j) dst[j * kWave] = h[j];
         }
         const float2 dh = sDH[r][cl];
-        float y = fwd_update<S, NPL>(h, hbp, gp, sTab, dh.x, dh.y, &sB[r][s * NPL],
-                                     &sC[r][s * NPL], s, p.NR, has_imag);
+        float y = fwd_update<S, NPL, GK>(h, hbp, gp, sTab, dh.x, dh.y, &sB[r][s * NPL],
+                                         &sC[r][s * NPL], s, p.NR, has_imag);
         y = reduce_states<S>(y);
         if (s == 0 && cvalid) {
           const int t = dir ? (L - 1 - i) : i;
@@ -123,16 +123,19 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   }
 }
 
-template <int S, int NPL>
+template <int S, int NPL, class GK>
 static hipError_t launch_fwd_t(const ScanParams& p, const FwdOut& o, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ntiles * p.B));
-  hipLaunchKernelGGL((scan_fwd_kernel<S, NPL>), grid, dim3(kThreads), 0, st, p, o);
+  hipLaunchKernelGGL((scan_fwd_kernel<S, NPL, GK>), grid, dim3(kThreads), 0, st, p, o);
   return hipGetLastError();
 }
 
-hipError_t launch_scan_fwd(int S, int NPL, const ScanParams& p, const FwdOut& o, hipStream_t st) {
-#define RP_CASE(SS, NN) \
-  if (S == SS && NPL == NN) return launch_fwd_t<SS, NN>(p, o, st);
+hipError_t launch_scan_fwd(int S, int NPL, bool spec, const ScanParams& p, const FwdOut& o,
+                           hipStream_t st) {
+#define RP_CASE(SS, NN)                                                          \
+  if (S == SS && NN == NPL)                                                      \
+    return spec ? launch_fwd_t<SS, NN, GateKind<NN - 1, 1>>(p, o, st)            \
+                : launch_fwd_t<SS, NN, GateKind<0, 2>>(p, o, st);
   RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
   return hipErrorInvalidValue;

