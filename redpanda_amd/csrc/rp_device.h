@@ -38,7 +38,6 @@ namespace rp {
 constexpr float kLog2e = 1.44269504088896340736f;
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr float kTwoPi = 6.28318530717958647692f;
-constexpr double kInv2PiD = 0.15915494309189533577;
 
 template <int S, int NPL>
 struct Shape {
@@ -92,12 +91,19 @@ __device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
 __device__ __forceinline__ void load_gate_params(const float* Ar, const float* Ai, const float* Tk,
                                                  int c, int n, int N, int NR, int NT, bool valid,
                                                  float& pah, float& wh) {
+  // x * K with K split as kHi + kLo: one rounding of the extended product
+  constexpr float kL2eHi = 1.4426950216293335f, kL2eLo = 1.925963033500011e-08f;  // log2(e)
+  constexpr float kW16Hi = 2.5464789867401123f, kW16Lo = 1.0273021189277642e-07f;   // 16/(2 pi)
   pah = 0.f;
   wh = 0.f;
   if (!valid) return;
   if (n < NR) {
-    pah = (float)((double)Ar[(int64_t)c * NR + n] * 1.4426950408889634074);
-    if (Ai != nullptr) wh = (float)((double)Ai[(int64_t)c * NR + n] * (16.0 * kInv2PiD));
+    const float a = Ar[(int64_t)c * NR + n];
+    pah = ffma(a, kL2eHi, fmul(a, kL2eLo));
+    if (Ai != nullptr) {
+      const float w = Ai[(int64_t)c * NR + n];
+      wh = ffma(w, kW16Hi, fmul(w, kW16Lo));
+    }
   } else if (n < N) {
     pah = Tk[(int64_t)c * NT + (n - NR)];
   }

@@ -75,8 +75,14 @@ struct StepParams {
   float* h_out;
   float* beta_out;
   float* y;
-  int ntiles;
+  int ntiles;   // lane-layout kernel: channel tiles of CB
+  int ctiles;   // tile kernel: channel tiles of kStepTile
+  int ri;       // tile kernel: rollouts per workgroup
+  int rgroups;  // tile kernel: ceil(R / ri)
 };
+
+// Channels (one per thread) of the step tile kernel's workgroup.
+constexpr int kStepTile = kThreads;
 
 // Chosen lane split for a state dimension N: S lanes per channel holding NPL
 // states each.  Returns false when N is beyond the compiled shapes.
@@ -92,7 +98,10 @@ hipError_t launch_scan_bwd(int S, int NPL, bool spec, const ScanParams& p, const
                            hipStream_t st);
 hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
                                float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st);
-hipError_t launch_step(int S, int NPL, bool spec, const StepParams& p, hipStream_t st);
+// `tile`: the thread-per-channel kernel (N == S*NPL, N % 4 == 0, N <= 40,
+// 16-byte aligned state pointers); otherwise the lane-layout kernel.
+// Bitwise the same.
+hipError_t launch_step(int S, int NPL, bool spec, bool tile, const StepParams& p, hipStream_t st);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 
 }  // namespace rp
