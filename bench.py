@@ -55,9 +55,10 @@ def parse():
     ap.add_argument("--no-step", action="store_true", help="skip the step() workload")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
-    ap.add_argument("--calib-copy", action="store_true",
-                    help="also run one plain 1 GiB device copy (reads 1 GiB, writes 1 GiB): "
-                         "the reference dispatch that scales FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="counter pass: run each kernel of the path a few times at the bench "
+                         "shapes plus one elementwise pass over 1 GiB (torch.neg: the reference "
+                         "dispatch that scales FETCH_SIZE / WRITE_SIZE), then exit")
     return ap.parse_args()
 
 
@@ -198,20 +199,21 @@ def bench_scan(torch, args, dtype):
     fb, bb = scan_bytes(B, L, D, N, NR, NT, s_in, True)
     kern = [
         {"kernel": "scan_fwd_kernel (bidirectional, checkpoints)", "seconds": t_fwd,
-         "alg_bytes": fb, "GBps": fb / t_fwd / 1e9},
+         "alg_bytes": fb, "GBps": fb / t_fwd / 1e9, "traffic_key": "scan_fwd_kernel"},
         {"kernel": "scan_fwd_kernel (bidirectional, inference)", "seconds": t_inf,
-         "alg_bytes": fb, "GBps": fb / t_inf / 1e9},
+         "alg_bytes": fb, "GBps": fb / t_inf / 1e9, "traffic_key": None},
         {"kernel": "scan_bwd_kernel + reductions", "seconds": t_bwd,
-         "alg_bytes": bb, "GBps": bb / t_bwd / 1e9},
+         "alg_bytes": bb, "GBps": bb / t_bwd / 1e9, "traffic_key": "scan_bwd_kernel+reductions"},
     ]
     return dict(tok_s=tok_s, elapsed=elapsed, kernels=kern, t_fwd=t_fwd, t_bwd=t_bwd,
                 t_inf=t_inf, fwd_bytes=fb, bwd_bytes=bb, T=B * L)
 
 
-def bench_step(torch, args):
+def bench_step(torch, args, layers=None, plies=32, keep=True):
     from redpanda_amd import _lib
     sh = STEP_SHAPE
-    R, layers, D, NR, NT = sh["R"], sh["layers"], sh["D"], sh["NR"], sh["NT"]
+    R, D, NR, NT = sh["R"], sh["D"], sh["NR"], sh["NT"]
+    layers = sh["layers"] if layers is None else layers
     N = NR + NT
     dev = torch.device("cuda:0")
     gen = torch.Generator().manual_seed(1004)
@@ -253,7 +255,8 @@ def bench_step(torch, args):
     for _ in range(max(args.warmup, 1)):
         ply()
     torch.cuda.synchronize()
-    plies = 32
+    if not keep:  # counter pass: the warm-up dispatches are the sample
+        return layers * max(args.warmup, 1)
     t0 = time.perf_counter()
     for _ in range(plies):
         ply()
@@ -264,6 +267,67 @@ def bench_step(torch, args):
     nb = step_bytes(R, D, N, NR, NT)
     return dict(rollout_steps_s=R * plies / elapsed, plies=plies, elapsed=elapsed,
                 t_launch=t_launch, bytes=nb, GBps=nb / t_launch / 1e9)
+
+
+def measured_traffic():
+    """HBM bytes per launch from the committed counter summary
+    (profiles/traffic.json, written by `python -m redpanda_amd.profiling
+    traffic` from FETCH_SIZE / WRITE_SIZE passes over `bench.py
+    --profile-pass`), or {} when there is none."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as fh:
+            k = json.load(fh)["kernels"]
+    except (OSError, KeyError, ValueError):
+        return {}
+    out = {name: v["bytes"] for name, v in k.items()}
+    if "scan_bwd_kernel" in k:
+        out["scan_bwd_kernel+reductions"] = sum(
+            k[n]["bytes"] for n in ("scan_bwd_kernel", "bwd_reduce_bc", "bwd_reduce_par") if n in k)
+    return out
+
+
+def profile_pass(torch):
+    """A few dispatches of every kernel at the bench shapes, for counter runs
+    (rocprofv3 --pmc collects per dispatch), then one 1 GiB device copy."""
+    from redpanda_amd import _lib
+    from redpanda_amd.scan import make_scan_args
+    sh = SCAN_SHAPE
+    B, L, D, NR, NT = sh["B"], sh["L"], sh["D"], sh["NR"], sh["NT"]
+    N = NR + NT
+    dev = torch.device("cuda:0")
+    c = scan_inputs(B, L, D, NR, NT, 1003, dev, torch.bfloat16)
+    lib = _lib.load()
+    f32 = dict(dtype=torch.float32, device=dev)
+    a = make_scan_args(c["delta"], c["u"], c["Bc"], c["Cc"], c["Ar"], c["Ai"], c["Tk"], True)
+    y = torch.empty((B, L, D), **f32)
+    ckpt = torch.empty(max(lib.rp_scan_ckpt_bytes(ctypes.byref(a)) // 4, 1), **f32)
+    g = [torch.empty((B, L, D), **f32), torch.empty((B, L, D), **f32),
+         torch.empty((B, L, N), **f32), torch.empty((B, L, N), **f32),
+         torch.empty((D, NR), **f32), torch.empty((D, NR), **f32), torch.empty((D, NT), **f32)]
+    work = torch.empty(max(lib.rp_scan_bwd_work_bytes(ctypes.byref(a)), 256), dtype=torch.uint8,
+                       device=dev)
+    out = _lib.ScanFwdOut(y.data_ptr(), ckpt.data_ptr(), None, None)
+    io = _lib.ScanBwdIO(dy=c["dy"].data_ptr(), ckpt=ckpt.data_ptr(), d_delta=g[0].data_ptr(),
+                        d_u=g[1].data_ptr(), d_Bc=g[2].data_ptr(), d_Cc=g[3].data_ptr(),
+                        d_A_real=g[4].data_ptr(), d_A_imag=g[5].data_ptr(),
+                        d_track=g[6].data_ptr(), work=work.data_ptr(), work_bytes=work.numel())
+    stream = _lib.stream_of(dev)
+    for _ in range(3):
+        _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out), stream), lib)
+        _lib.check(lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), stream), lib)
+    torch.cuda.synchronize()
+    del y, ckpt, g, work, c
+    args = argparse.Namespace(warmup=3)
+    step_layers = bench_step(torch, args, layers=1, plies=3, keep=False)
+    # calibration: one elementwise dispatch that reads 1 GiB and writes 1 GiB
+    # (a device-to-device copy_ is split into several copy dispatches)
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print(f"[bench] profile pass done: scan fwd/bwd x3, step x{step_layers}, "
+          f"calibration neg {src.numel() * 4} bytes each way", file=sys.stderr, flush=True)
 
 
 def cpu_baseline(budget_s):
@@ -330,6 +394,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no ROCm GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.profile_pass:
+        profile_pass(torch)
+        return
     print(f"[bench] scan fwd+bwd {SCAN_SHAPE} bf16 storage, steps={args.steps} "
           f"warmup={args.warmup}", file=sys.stderr, flush=True)
     sc = bench_scan(torch, args, torch.bfloat16)
@@ -352,9 +419,10 @@ def main():
     # dominant kernel: the longer of forward (training) and backward
     k_f, k_b = sc["kernels"][0], sc["kernels"][2]
     dom = k_b if k_b["seconds"] >= k_f["seconds"] else k_f
+    tr = measured_traffic()
     roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["GBps"] / HBM_PEAK_GBS,
-            "traffic": None, "alg_bytes_per_launch": dom["alg_bytes"],
+            "traffic": tr.get(dom["traffic_key"]), "alg_bytes_per_launch": dom["alg_bytes"],
             "avg_launch_s": dom["seconds"]}
     ms = sc["elapsed"] / args.steps * 1e3
     line = {
@@ -378,19 +446,12 @@ def main():
                        **STEP_SHAPE, "d_state": STEP_SHAPE["NR"] + STEP_SHAPE["NT"]},
             "roofline": {"bound": "hbm", "kernel": "step_kernel",
                          "achieved": step["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": step["GBps"] / HBM_PEAK_GBS, "traffic": None,
+                         "frac": step["GBps"] / HBM_PEAK_GBS,
+                         "traffic": tr.get("step_tile_kernel"),
                          "alg_bytes_per_launch": step["bytes"],
                          "avg_launch_s": step["t_launch"]},
         }
     line["cpu_baseline"] = cpu
-    if args.calib_copy:
-        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        print(f"[bench] calibration copy: {src.numel() * 4} bytes read and written",
-              file=sys.stderr, flush=True)
-        del src, dst
     print(json.dumps(line), flush=True)
 
 
