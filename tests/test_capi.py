@@ -166,3 +166,18 @@ def _header_struct_fields(name):
 def test_ctypes_structs_mirror_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
     assert py == _header_struct_fields(cname)
+
+
+def test_triton_scan_module_names():
+    """The names the reference's callers import from `triton_scan`
+    (engine/mamba.py:344, engine/train.py:711) exist with the same call shape."""
+    import inspect
+
+    from redpanda_amd import triton_scan
+
+    for name in ("HAS_TRITON", "triton_trapezoidal_scan", "verify"):
+        assert hasattr(triton_scan, name)
+    params = list(inspect.signature(triton_scan.triton_trapezoidal_scan).parameters)
+    assert params[:9] == ["delta", "u", "B_contracted", "C_contracted", "A_real", "A_imag",
+                          "track", "n_rot", "n_state"]
+    assert list(inspect.signature(triton_scan.verify).parameters) == ["device", "thorough", "verbose"]
