@@ -42,26 +42,27 @@ def _torch_lib_dir():
         return os.path.join(sysconfig.get_paths()["purelib"], "torch", "lib")
 
 
-def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+def sources(csrc=CSRC):
+    return sorted(os.path.join(csrc, f) for f in os.listdir(csrc) if f.endswith(".hip"))
 
 
-def build(verbose=False, extra_flags=()):
-    """Compile and link; returns the library path.  Raises on any failure."""
-    srcs = sources()
+def build(verbose=False, extra_flags=(), csrc=CSRC, out=LIB_PATH):
+    """Compile the .hip files of `csrc` and link them into `out` (by default
+    the package's library); returns the library path.  Raises on any failure."""
+    srcs = sources(csrc)
     tmp = tempfile.mkdtemp(prefix="rp_build_")
     objs, procs = [], []
     for src in srcs:
         obj = os.path.join(tmp, os.path.basename(src) + ".o")
-        cmd = [HIPCC, *DEVICE_FLAGS, *extra_flags, "-I", INCLUDE, "-I", CSRC, "-c", src, "-o", obj]
+        cmd = [HIPCC, *DEVICE_FLAGS, *extra_flags, "-I", INCLUDE, "-I", csrc, "-c", src, "-o", obj]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
     failed = []
     for src, pr in procs:
-        out, _ = pr.communicate()
-        text = out.decode(errors="replace")
+        log, _ = pr.communicate()
+        text = log.decode(errors="replace")
         # the host pass does not know the device-only target feature: harmless
         text = "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l)
         if pr.returncode != 0:
@@ -72,7 +73,7 @@ def build(verbose=False, extra_flags=()):
         msg = "\n".join(f"--- {s}\n{t}" for s, t in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
     tl = _torch_lib_dir()
-    tmp_lib = LIB_PATH + ".tmp"
+    tmp_lib = out + ".tmp"
     link = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_lib,
             "-L", tl, "-Wl,-rpath," + tl, "-Wl,--no-undefined"]
     if verbose:
@@ -80,11 +81,11 @@ def build(verbose=False, extra_flags=()):
     res = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stdout.decode(errors="replace"))
-    os.replace(tmp_lib, LIB_PATH)
+    os.replace(tmp_lib, out)
     for o in objs:
         os.remove(o)
     os.rmdir(tmp)
-    return LIB_PATH
+    return out
 
 
 if __name__ == "__main__":

@@ -59,7 +59,7 @@ int step_ri_override() {
 
 struct Plan {
   int S, NPL, CB, ntiles, nck, ndir, bg, nbg;
-  bool spec;  // compile-time rotational / tracking split (see launch_scan_fwd)
+  int gk;     // gate kind: rotational / tracking split fixed at compile time
   int64_t ckpt_bytes, part_bc_bytes, part_par_bytes;
 };
 
@@ -124,7 +124,7 @@ Plan make_plan(const rp_scan_args* a) {
   pl.S = S;
   pl.NPL = NPL;
   pl.CB = rp::kWaves * (rp::kWave / S);
-  pl.spec = a->A_imag != nullptr && a->NR >= (int64_t)S * (NPL - 1);
+  pl.gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
   pl.ntiles = (int)((a->D + pl.CB - 1) / pl.CB);
   const int64_t nchunks = (a->L + rp::kCkptK - 1) / rp::kCkptK;
   pl.nck = (int)(nchunks > 0 ? nchunks - 1 : 0);
@@ -263,7 +263,7 @@ int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream)
     return fail(RP_ERR_UNSUPPORTED, "scan fwd: grid too large");
   const rp::ScanParams p = scan_params(a, pl);
   rp::FwdOut o{out->y, pl.ckpt_bytes > 0 ? out->ckpt : nullptr, out->h_last, out->beta_last};
-  hipError_t e = rp::launch_scan_fwd(pl.S, pl.NPL, pl.spec, p, o, (hipStream_t)stream);
+  hipError_t e = rp::launch_scan_fwd(pl.S, pl.NPL, pl.gk, p, o, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "scan fwd launch");
   return RP_OK;
 }
@@ -318,7 +318,7 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
   b.nbg = pl.nbg;
   hipStream_t s = (hipStream_t)stream;
   if (a->B > 0) {
-    hipError_t e = rp::launch_scan_bwd(pl.S, pl.NPL, pl.spec, p, b, s);
+    hipError_t e = rp::launch_scan_bwd(pl.S, pl.NPL, pl.gk, p, b, s);
     if (e != hipSuccess) return fail_hip(e, "scan bwd launch");
   }
   hipError_t e = rp::launch_bwd_finalize(p, b, io->d_Bc, io->d_Cc,
@@ -389,7 +389,7 @@ int rp_step(const rp_step_args* a, void* stream) {
   p.ntiles = (int)((a->D + CB - 1) / CB);
   if ((int64_t)p.ntiles * a->R > kI32Max)
     return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
-  const bool spec = a->A_imag != nullptr && a->NR >= (int64_t)S * (NPL - 1);
+  const int gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
   // the tile kernel moves each channel's (h, beta) as 16-byte vectors
   const bool tile = a->N % 4 == 0 && S * NPL == a->N && a->N <= 40 && aligned(a->h_out, 16) &&
                     aligned(a->beta_out, 16) &&
@@ -411,7 +411,7 @@ int rp_step(const rp_step_args* a, void* stream) {
     if ((int64_t)p.ctiles * p.rgroups > kI32Max)
       return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   }
-  hipError_t e = rp::launch_step(S, NPL, spec, tile, p, (hipStream_t)stream);
+  hipError_t e = rp::launch_step(S, NPL, gk, tile, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "step launch");
   return RP_OK;
 }

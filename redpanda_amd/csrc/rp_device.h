@@ -49,14 +49,23 @@ struct Shape {
   static_assert(S == 2 || S == 4 || S == 8 || S == 16, "S must be a power of two <= 16");
 };
 
+// Streamed-input element as stored (fp32 bits, or a bf16 / fp16 pattern in
+// the low half), and its fp32 value; split so that a load can be issued well
+// before its value is needed.
+__device__ __forceinline__ uint32_t load_raw(const void* p, int64_t i, int dtype) {
+  if (dtype == RP_F32) return __float_as_uint(static_cast<const float*>(p)[i]);
+  return static_cast<const uint16_t*>(p)[i];
+}
+
+__device__ __forceinline__ float cvt_raw(uint32_t v, int dtype) {
+  if (dtype == RP_F32) return __uint_as_float(v);
+  if (dtype == RP_BF16) return __uint_as_float(v << 16);
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v)));
+}
+
 // Streamed-input load with on-the-fly conversion to fp32 (uniform dtype).
 __device__ __forceinline__ float load_in(const void* p, int64_t i, int dtype) {
-  if (dtype == RP_F32) return static_cast<const float*>(p)[i];
-  if (dtype == RP_BF16) {
-    const uint32_t bits = static_cast<const uint16_t*>(p)[i];
-    return __uint_as_float(bits << 16);
-  }
-  return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  return cvt_raw(load_raw(p, i, dtype), dtype);
 }
 
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }
@@ -120,15 +129,18 @@ constexpr float kS1 = 0.39269908169872414f, kS3 = -0.010093189023535096f,
 
 // How a kernel instantiation knows the rotational / tracking split:
 //   RJ   leading state slots j < RJ are rotational in every lane (compile
-//        time); slots j >= RJ are decided at run time from NR;
+//        time);
+//   TJ   trailing slots j >= TJ are tracking (or padding) in every lane
+//        (compile time); slots RJ <= j < TJ are decided at run time from NR;
 //   IMAG 1: complex rotational gates, 0: real decay gates, 2: decided at
 //        run time from has_imag.
 // Specialised and generic instantiations run the same arithmetic, so their
 // results are bitwise equal.
-template <int RJ, int IMAG>
+template <int RJ, int IMAG, int TJ>
 struct GateKind {
   static constexpr int kRJ = RJ;
   static constexpr int kImag = IMAG;
+  static constexpr int kTJ = TJ;
 };
 
 // Rotational gate g = 2^(dt pah) cos(pi/8 dt wh); with WITH_SIN also
@@ -136,38 +148,74 @@ struct GateKind {
 // exactly into an integer k (the table index, by the round-to-integer
 // addition) and a remainder |r| <= 1/2.  The cos path is the same code in
 // both instantiations, so g is bitwise the same.
-template <bool WITH_SIN>
-__device__ __forceinline__ float rot_gate(float dt, float pah, float wh, bool imag,
-                                          const float2* tab, float& es) {
-  const float e = exp2_hw(fmul(dt, pah));
+//
+// The gate is split in two phases so that a caller can start the
+// exponentials and table reads of several states before finishing any of
+// them (rot_gate_issue, then rot_gate_finish); rot_gate is the two in a row.
+struct GatePart {
+  float e;    // 2^(dt pah)
+  float r;    // angle remainder, |r| <= 1/2 (1/16 revolutions)
+  float2 cs;  // cos, sin of the table angle
+};
+
+__device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh, bool imag,
+                                                   const float2* tab) {
+  GatePart g;
+  g.e = exp2_hw(fmul(dt, pah));
   if (!imag) {
-    es = 0.f;
-    return e;
+    g.r = 0.f;
+    g.cs = make_float2(1.f, 0.f);
+    return g;
   }
   const float w = fmul(dt, wh);
   const float t = w + kRint;
-  const float kf = t - kRint;                    // rint(w), exact
-  const float r = w - kf;                        // exact
+  const float kf = t - kRint;  // rint(w), exact
+  g.r = w - kf;                // exact
+  g.cs = tab[__float_as_int(t) & 15];
+  return g;
+}
+
+template <bool WITH_SIN>
+__device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag, float& es) {
+  if (!imag) {
+    es = 0.f;
+    return g.e;
+  }
+  const float r = g.r;
   const float r2 = fmul(r, r);
   const float cm1 = fmul(r2, ffma(r2, ffma(r2, kC6, kC4), kC2));  // cos - 1
   const float sx = fmul(r, ffma(r2, ffma(r2, kS5, kS3), kS1));    // sin
-  const float2 cs = tab[__float_as_int(t) & 15];
-  const float cv = ffma(-cs.y, sx, ffma(cs.x, cm1, cs.x));
+  const float cv = ffma(-g.cs.y, sx, ffma(g.cs.x, cm1, g.cs.x));
   if (WITH_SIN) {
-    const float sv = ffma(cs.x, sx, ffma(cs.y, cm1, cs.y));
-    es = fmul(e, sv);
+    const float sv = ffma(g.cs.x, sx, ffma(g.cs.y, cm1, g.cs.y));
+    es = fmul(g.e, sv);
   } else {
     es = 0.f;
   }
-  return fmul(e, cv);
+  return fmul(g.e, cv);
+}
+
+template <bool WITH_SIN>
+__device__ __forceinline__ float rot_gate(float dt, float pah, float wh, bool imag,
+                                          const float2* tab, float& es) {
+  return rot_gate_finish<WITH_SIN>(rot_gate_issue(dt, pah, wh, imag, tab), imag, es);
 }
 
 // Whether state slot j of lane slice s is rotational (n = j*S + s < NR).
 template <int S, class GK>
 __device__ __forceinline__ bool is_rot(int j, int s, int NR) {
+  if (j >= GK::kTJ) return false;
   if (j < GK::kRJ) return true;
   if (j * S >= NR) return false;
   return (j + 1) * S <= NR || j * S + s < NR;
+}
+
+// Host side: calls f(GK{}) with the GateKind instantiation of gate code gk.
+template <int NPL, class F>
+hipError_t with_gate_kind(int gk, F&& f) {
+  if (gk == kGateRotTrack) return f(GateKind<NPL - 1, 1, NPL - 1>{});
+  if (gk == kGateRotLead) return f(GateKind<NPL - 1, 1, NPL>{});
+  return f(GateKind<0, 2, NPL>{});
 }
 
 template <class GK>
@@ -180,12 +228,44 @@ __device__ __forceinline__ bool imag_of(bool has_imag) {
 template <int S, class GK, bool WITH_SIN>
 __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pah,
                                          float wh, const float2* tab, float& es) {
+  if (j >= GK::kTJ) {
+    es = 0.f;
+    return pah;
+  }
   if (j < GK::kRJ) return rot_gate<WITH_SIN>(dt, pah, wh, imag_of<GK>(has_imag), tab, es);
   if (j * S >= NR) {
     es = 0.f;
     return pah;
   }
   const float gr = rot_gate<WITH_SIN>(dt, pah, wh, imag_of<GK>(has_imag), tab, es);
+  if ((j + 1) * S <= NR || j * S + s < NR) return gr;
+  es = 0.f;
+  return pah;
+}
+
+// gate_of in two phases (see rot_gate_issue): gate_issue starts the
+// rotational part of slot j, gate_finish returns the gate; the pair computes
+// exactly gate_of.
+template <int S, class GK>
+__device__ __forceinline__ GatePart gate_issue(int j, int NR, bool has_imag, float dt, float pah,
+                                               float wh, const float2* tab) {
+  if (j >= GK::kTJ || (j >= GK::kRJ && j * S >= NR)) return GatePart{0.f, 0.f, {1.f, 0.f}};
+  return rot_gate_issue(dt, pah, wh, imag_of<GK>(has_imag), tab);
+}
+
+template <int S, class GK, bool WITH_SIN>
+__device__ __forceinline__ float gate_finish(int j, int s, int NR, bool has_imag,
+                                             const GatePart& part, float pah, float& es) {
+  if (j >= GK::kTJ) {
+    es = 0.f;
+    return pah;
+  }
+  if (j < GK::kRJ) return rot_gate_finish<WITH_SIN>(part, imag_of<GK>(has_imag), es);
+  if (j * S >= NR) {
+    es = 0.f;
+    return pah;
+  }
+  const float gr = rot_gate_finish<WITH_SIN>(part, imag_of<GK>(has_imag), es);
   if ((j + 1) * S <= NR || j * S + s < NR) return gr;
   es = 0.f;
   return pah;

@@ -10,10 +10,9 @@ constexpr int kWave = 64;
 constexpr int kWaves = 4;  // waves per workgroup
 constexpr int kThreads = kWave * kWaves;
 
-// Time steps staged in LDS per block by the forward and backward kernels,
-// and the checkpoint interval of the backward's recompute.
+// Time steps staged in LDS per block by the forward kernel, and the
+// checkpoint interval (the chunk) of the backward's recompute.
 constexpr int kFwdTB = 32;
-constexpr int kBwdTB = 16;
 constexpr int kCkptK = 4;
 
 struct ScanParams {
@@ -88,20 +87,31 @@ constexpr int kStepTile = kThreads;
 // states each.  Returns false when N is beyond the compiled shapes.
 bool choose_shape(int N, int* S, int* NPL);
 
-// `spec`: every state slot j < NPL-1 is rotational in every lane (NR >=
-// S*(NPL-1)) and the gates are complex; selects the instantiation that
-// resolves the rotational / tracking split at compile time (bitwise the
-// same results as the generic one).
-hipError_t launch_scan_fwd(int S, int NPL, bool spec, const ScanParams& p, const FwdOut& o,
+// Gate kind of a launch: how much of the rotational / tracking split of the
+// state slots is fixed at compile time.  Every kind gives bitwise the same
+// results; the specialised ones drop run-time selects and dead gate code.
+enum GateCode {
+  kGateGeneric = 0,   // every slot decided at run time
+  kGateRotLead = 1,   // complex gates, slots j < NPL-1 rotational (NR >= S*(NPL-1))
+  kGateRotTrack = 2,  // complex gates, slots j < NPL-1 rotational, slot NPL-1
+                      // tracking or padding (NR == S*(NPL-1))
+};
+
+inline int gate_code(bool has_imag, int64_t NR, int S, int NPL) {
+  if (!has_imag || NR < (int64_t)S * (NPL - 1)) return kGateGeneric;
+  return NR == (int64_t)S * (NPL - 1) ? kGateRotTrack : kGateRotLead;
+}
+
+hipError_t launch_scan_fwd(int S, int NPL, int gk, const ScanParams& p, const FwdOut& o,
                            hipStream_t st);
-hipError_t launch_scan_bwd(int S, int NPL, bool spec, const ScanParams& p, const BwdIO& io,
+hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const BwdIO& io,
                            hipStream_t st);
 hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
                                float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st);
 // `tile`: the thread-per-channel kernel (N == S*NPL, N % 4 == 0, N <= 40,
 // 16-byte aligned state pointers); otherwise the lane-layout kernel.
 // Bitwise the same.
-hipError_t launch_step(int S, int NPL, bool spec, bool tile, const StepParams& p, hipStream_t st);
+hipError_t launch_step(int S, int NPL, int gk, bool tile, const StepParams& p, hipStream_t st);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 
 }  // namespace rp

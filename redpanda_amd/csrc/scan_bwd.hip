@@ -21,12 +21,21 @@
 // the forward's gate code (with the sine added), so it rebuilds the forward's
 // states exactly.
 //
+// Streaming: the per-step inputs (dt, (dt*u)/2, u, dy per channel; B, C per
+// state) of a chunk and of the step before it sit in one of two LDS slots.
+// While chunk c is computed from its slot, the inputs of chunk c-1 are loaded
+// into registers and written to the other slot after the compute, so
+// global-memory latency hides behind a whole chunk; the checkpoint entering
+// the next chunk and every value a read-modify-write needs (reverse
+// direction) are likewise loaded a chunk ahead.  The chunk code is
+// instantiated per slot, so every LDS address is a compile-time offset.
+//
 // Reductions, all in a fixed order (run-to-run deterministic, no atomics):
 //   * over a channel's states (ddt, du): in-lane FMA chain + DPP butterfly;
 //   * over channels (dB, dC): DPP row rotations inside each 16-lane row, the
 //     row partials staged in LDS, then a 16-way sum per output, per tile;
 //     the per-tile partials are summed in float64 by a second kernel;
-//   * parameter gradients (dA, dTk): 8-step fp32 chunk sums accumulated in
+//   * parameter gradients (dA, dTk): K-step fp32 chunk sums accumulated in
 //     float64 per lane over the batch group, then float64 across groups.
 
 #include <type_traits>
@@ -39,25 +48,31 @@ namespace rp {
 template <int S, int NPL, class GK>
 __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
   using Sh = Shape<S, NPL>;
-  constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = kBwdTB, K = kCkptK;
+  constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, K = kCkptK;
   constexpr int KR = NP <= 40 ? K : K / 2;  // steps per channel-sum fold
+  constexpr int NFOLD = K / KR;             // folds per chunk
   constexpr int NRW = kWaves * 4;           // 16-lane rows per workgroup
-  static_assert(TB % K == 0 && K % KR == 0, "time block must hold whole chunks");
-  // row 0 = the step just before the block (its (dt*u)/2 and B seed the
-  // trapezoid carry at the first chunk's entry); rows 1..TB = the block
-  __shared__ float4 sCh[TB + 1][CB];        // (dt, (dt*u)/2, u, dy)
-  __shared__ float sB[TB + 1][NP];
-  __shared__ float sC[TB + 1][NP];
-  __shared__ float sRed[KR][2][NRW][NP];    // per-row channel sums of dB, dC
-  __shared__ float2 sDD[TB][CB];            // (d_delta, d_u) of the block
-  __shared__ float2 sTab[16];               // cos, sin of 2 pi k / 16
+  constexpr int FPT = (KR * 2 * NP + kThreads - 1) / kThreads;  // fold outputs per thread
+  constexpr int KS = K + 1;  // staged steps per chunk: the step before it, then its K steps
+  constexpr int CPT = (KS * CB + kThreads - 1) / kThreads;      // staged channel-steps per thread
+  constexpr int SPT = (KS * NP + kThreads - 1) / kThreads;      // staged state-steps per thread
+  constexpr int DPT = (K * CB + kThreads - 1) / kThreads;       // d_delta / d_u outputs per thread
+  static_assert(K % KR == 0, "a chunk holds whole folds");
+  __shared__ float4 sCh[2][KS][CB];       // input slots: (dt, (dt*u)/2, u, dy)
+  __shared__ float sB[2][KS][NP];
+  __shared__ float sC[2][KS][NP];
+  __shared__ float sRed[KR][2][NRW][NP];  // per-row channel sums of dB, dC
+  __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
+  __shared__ float2 sTab[16];             // cos, sin of 2 pi k / 16
+  // per-thread float64 sums of the parameter gradients over the batch group
+  // (dA_real or dtrack, dA_imag), kept in LDS to spare registers
+  __shared__ double sPar[2][NPL][kThreads];
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
   const int dl = lane / S, s = lane % S;
   const int cl = wave * DT + dl;
-  const int wrow = wave * 4 + lane / 16;    // row index within the workgroup
-  const bool row_leader = (lane % 16) < S;  // first channel of its row
+  const int wrow = wave * 4 + lane / 16;  // row index within the workgroup
   const int tile = blockIdx.x % p.ntiles, bgi = blockIdx.x / p.ntiles;
   const int c = tile * CB + cl;
   const bool cvalid = c < p.D;
@@ -67,16 +82,116 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   fill_sincos_table(sTab, tid);  // first read after the staging barrier below
   GateRegs<NPL> gp;
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
-  double dpa[NPL], dpb[NPL];
+  // pam: the coefficient of the ddt sum over rotational states, zero for a
+  // tracking state (only read for slots whose kind is decided at run time)
+  float pam[NPL];
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    dpa[j] = 0.0;
-    dpb[j] = 0.0;
+    pam[j] = is_rot<S, GK>(j, s, p.NR) ? gp.pah[j] : 0.f;
+    sPar[0][j][tid] = 0.0;
+    sPar[1][j][tid] = 0.0;
   }
+
+  // time index of forward-order step i in this direction
+  auto tix = [&](int dir, int i) { return dir ? (L - 1 - i) : i; };
+  // Inputs of chunk ch (rows 1..K) and of the step before it (row 0) as
+  // stored: loaded into registers (stage_load), then converted into an LDS
+  // slot (stage_store).  Steps and channels beyond the data load as zeros.
+  uint32_t rdt[CPT], ru[CPT], rb[SPT], rc[SPT];
+  float rdy[CPT];
+  auto stage_load = [&](int b, int dir, int ch) {
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int r = e / CB, ci = e % CB;
+      const int i = ch * K + r - 1, c2 = tile * CB + ci;
+      rdt[k] = 0u;
+      ru[k] = 0u;
+      rdy[k] = 0.f;
+      if (e < KS * CB && i >= 0 && i < L && c2 < p.D) {
+        const int t = tix(dir, i);
+        rdt[k] = load_raw(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
+        ru[k] = load_raw(p.u, (int64_t)b * p.usb + (int64_t)t * p.usl + c2, p.dt_u);
+        rdy[k] = io.dy[((int64_t)b * L + t) * p.D + c2];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int r = e / NP, kk = e % NP;
+      const int n = (kk % NPL) * S + (kk / NPL);
+      const int i = ch * K + r - 1;
+      rb[k] = 0u;
+      rc[k] = 0u;
+      if (e < KS * NP && i >= 0 && i < L && n < p.N) {
+        const int t = tix(dir, i);
+        rb[k] = load_raw(p.Bc, (int64_t)b * p.bsb + (int64_t)t * p.bsl + n, p.dt_B);
+        rc[k] = load_raw(p.Cc, (int64_t)b * p.csb + (int64_t)t * p.csl + n, p.dt_C);
+      }
+    }
+  };
+  auto stage_store = [&](auto slot_tag) {
+    constexpr int SL = decltype(slot_tag)::value;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int e = tid + k * kThreads;
+      if (e < KS * CB) {
+        const float dt = cvt_raw(rdt[k], p.dt_delta);
+        const float uu = cvt_raw(ru[k], p.dt_u);
+        sCh[SL][e / CB][e % CB] = make_float4(dt, 0.5f * fmul(dt, uu), uu, rdy[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int e = tid + k * kThreads;
+      if (e < KS * NP) {
+        sB[SL][e / NP][e % NP] = cvt_raw(rb[k], p.dt_B);
+        sC[SL][e / NP][e % NP] = cvt_raw(rc[k], p.dt_C);
+      }
+    }
+  };
+  using Slot0 = std::integral_constant<int, 0>;
+  using Slot1 = std::integral_constant<int, 1>;
+  // h entering chunk `chunk` of this lane's states: the forward's checkpoint,
+  // or for chunk 0 the initial state (zero unless h0 is given, causal only)
+  auto load_entry_h = [&](int chunk, int b, int dir, float (&dst)[NPL]) {
+    if (chunk == 0) {
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        const int n = j * S + s;
+        dst[j] = 0.f;
+        if (dir == 0 && p.h0 != nullptr && cvalid && n < p.N)
+          dst[j] = p.h0[((int64_t)b * p.D + c) * p.N + n];
+      }
+    } else {
+      const int64_t rec = ((int64_t)(dir * p.B + b) * p.nck + (chunk - 1)) * p.ntiles + tile;
+      const float* src = io.ckpt + (rec * kWaves + wave) * (NPL * kWave) + lane;
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) dst[j] = src[j * kWave];
+    }
+  };
+  // The (which, t, n) partial of tile `tile`, batch row b that fold output e
+  // of the fold starting at chunk step mf writes; null when beyond the chunk.
+  auto fold_dst = [&](int e, int b, int dir, int i0, int mf, int kcnt) -> float* {
+    const int rr = e / (2 * p.N);
+    if (e >= KR * 2 * p.N || mf + rr >= kcnt) return nullptr;
+    const int rem = e % (2 * p.N);
+    const int which = rem / p.N, n = rem % p.N;
+    const int t = tix(dir, i0 + mf + rr);
+    return io.part_bc + (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
+           (int64_t)t * p.N + n;
+  };
+  // The d_delta / d_u element of chunk step e / CB, channel e % CB; -1 when
+  // beyond the chunk or the channels.
+  auto dd_index = [&](int e, int b, int dir, int i0, int kcnt) -> int64_t {
+    const int r = e / CB, c2 = tile * CB + e % CB;
+    if (e >= K * CB || r >= kcnt || c2 >= p.D) return -1;
+    return ((int64_t)b * L + tix(dir, i0 + r)) * p.D + c2;
+  };
 
   const int b_lo = bgi * io.bg;
   const int b_hi = min(p.B, b_lo + io.bg);
-  const int nblk = (L + TB - 1) / TB;
+  const int nct = (L + K - 1) / K;  // chunks per sweep
 
   for (int b = b_lo; b < b_hi; ++b) {
     for (int dir = 0; dir < p.ndir; ++dir) {
@@ -95,209 +210,212 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           if (io.dbeta_last != nullptr) gr[j] = 2.f * io.dbeta_last[idx];
         }
       }
-
-      for (int bi = nblk - 1; bi >= 0; --bi) {
-        const int i0 = bi * TB;
-        const int cnt = min(TB, L - i0);
+      // the entry state of the next chunk to process, loaded one chunk ahead
+      float hnx[NPL];
+      if (nct > 0) {
+        load_entry_h(nct - 1, b, dir, hnx);
+        // stage the sweep's first chunk (the slots are free: the previous
+        // sweep ended with a barrier)
+        stage_load(b, dir, nct - 1);
+        if ((nct - 1) % 2 == 0)
+          stage_store(Slot0{});
+        else
+          stage_store(Slot1{});
         __syncthreads();
-        for (int e = tid; e < (TB + 1) * CB; e += kThreads) {
-          const int r = e / CB, ci = e % CB;
-          const int c2 = tile * CB + ci;
-          const int i = i0 + r - 1;
-          float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (r <= cnt && i >= 0 && c2 < p.D) {
-            const int t = dir ? (L - 1 - i) : i;
-            const float dt = load_in(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
-            const float uu = load_in(p.u, (int64_t)b * p.usb + (int64_t)t * p.usl + c2, p.dt_u);
-            v.x = dt;
-            v.y = 0.5f * fmul(dt, uu);
-            v.z = uu;
-            v.w = io.dy[((int64_t)b * L + t) * p.D + c2];
-          }
-          sCh[r][ci] = v;
-        }
-        for (int e = tid; e < (TB + 1) * NP; e += kThreads) {
-          const int r = e / NP, k = e % NP;
-          const int n = (k % NPL) * S + (k / NPL);
-          const int i = i0 + r - 1;
-          float bv = 0.f, cv = 0.f;
-          if (r <= cnt && i >= 0 && n < p.N) {
-            const int t = dir ? (L - 1 - i) : i;
-            bv = load_in(p.Bc, (int64_t)b * p.bsb + (int64_t)t * p.bsl + n, p.dt_B);
-            cv = load_in(p.Cc, (int64_t)b * p.csb + (int64_t)t * p.csl + n, p.dt_C);
-          }
-          sB[r][k] = bv;
-          sC[r][k] = cv;
-        }
-        __syncthreads();
+      }
 
-        const int nchunk = (cnt + K - 1) / K;
-        for (int kc = nchunk - 1; kc >= 0; --kc) {
-          const int m0 = kc * K;
-          const int kcnt = min(K, cnt - m0);
-          const int chunk = (i0 + m0) / K;
-          // state entering the chunk: h from the forward's checkpoint, hb
-          // recomputed from the step before (row m0 of the stage)
-          float hc[NPL], hbp[NPL];
-          if (chunk == 0) {
+      for (int ch = nct - 1; ch >= 0; --ch) {
+        const int i0 = ch * K;
+        const int kcnt = min(K, L - i0);
+        // loads a chunk ahead: the inputs of chunk ch-1, and the partials the
+        // reverse direction adds to (dB / dC and d_delta / d_u)
+        if (ch >= 1) stage_load(b, dir, ch - 1);
+        float prev[NFOLD][FPT], pdd[DPT][2];
+#pragma unroll
+        for (int f = 0; f < NFOLD; ++f) {
+#pragma unroll
+          for (int k = 0; k < FPT; ++k) {
+            prev[f][k] = 0.f;
+            if (dir == 1) {
+              const float* src = fold_dst(tid + k * kThreads, b, dir, i0, f * KR, kcnt);
+              if (src != nullptr) prev[f][k] = *src;
+            }
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < DPT; ++k) {
+          pdd[k][0] = 0.f;
+          pdd[k][1] = 0.f;
+          if (dir == 1) {
+            const int64_t idx = dd_index(tid + k * kThreads, b, dir, i0, kcnt);
+            if (idx >= 0) {
+              pdd[k][0] = io.d_delta[idx];
+              pdd[k][1] = io.d_u[idx];
+            }
+          }
+        }
+        // state entering the chunk: h as prefetched, hb from the step before
+        // (row 0 of the slot; zero before the first step) or, for chunk 0 of
+        // a causal scan from a given state, from beta0
+        float hc[NPL], hbp[NPL];
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) hc[j] = hnx[j];
+        if (ch > 0) load_entry_h(ch - 1, b, dir, hnx);
+        // The chunk body, instantiated for FULL (all K steps present, the
+        // common case; straight-line code) or a guarded tail for a last chunk
+        // shorter than K, and for the LDS slot SL that holds the chunk.
+        auto chunk_body = [&](auto full_tag, auto slot_tag) {
+          constexpr bool FULL = decltype(full_tag)::value;
+          constexpr int SL = decltype(slot_tag)::value;
+          if (ch == 0) {
 #pragma unroll
             for (int j = 0; j < NPL; ++j) {
               const int n = j * S + s;
-              hc[j] = 0.f;
               hbp[j] = 0.f;
-              if (dir == 0 && p.h0 != nullptr && cvalid && n < p.N) {
-                const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
-                hc[j] = p.h0[idx];
-                hbp[j] = 0.5f * p.beta0[idx];
-              }
+              if (dir == 0 && p.h0 != nullptr && cvalid && n < p.N)
+                hbp[j] = 0.5f * p.beta0[((int64_t)b * p.D + c) * p.N + n];
             }
           } else {
-            const int64_t rec = ((int64_t)(dir * p.B + b) * p.nck + (chunk - 1)) * p.ntiles + tile;
-            const float* src = io.ckpt + (rec * kWaves + wave) * (NPL * kWave) + lane;
-            const float hdp = sCh[m0][cl].y;
+            const float hdp = sCh[SL][0][cl].y;
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-              hc[j] = src[j * kWave];
-              hbp[j] = fmul(hdp, sB[m0][s * NPL + j]);
+            for (int j = 0; j < NPL; ++j) hbp[j] = fmul(hdp, sB[SL][0][s * NPL + j]);
+          }
+          // recompute the chunk: s_{t-1}, g_t and e*sin for every step
+          float SP[K][NPL], G[K][NPL], ES[K][NPL];
+#pragma unroll
+          for (int m = 0; m < K; ++m) {
+            if (FULL || m < kcnt) {
+              const float dt = sCh[SL][m + 1][cl].x;
+              const float hd = sCh[SL][m + 1][cl].y;
+              // start every state's exponential and table read, then finish
+              GatePart part[NPL];
+#pragma unroll
+              for (int j = 0; j < NPL; ++j)
+                part[j] = gate_issue<S, GK>(j, p.NR, has_imag, dt, gp.pah[j], gp.wh[j], sTab);
+#pragma unroll
+              for (int j = 0; j < NPL; ++j) {
+                float es;
+                const float g =
+                    gate_finish<S, GK, true>(j, s, p.NR, has_imag, part[j], gp.pah[j], es);
+                const float hb = fmul(hd, sB[SL][m + 1][s * NPL + j]);
+                const float sm = hc[j] + hbp[j];
+                SP[m][j] = sm;
+                G[m][j] = g;
+                ES[m][j] = es;
+                hc[j] = ffma(g, sm, hb);
+                hbp[j] = hb;
+              }
             }
           }
-          // The chunk body, instantiated twice: FULL (all K steps present, the
-          // common case; straight-line code) and a guarded tail for a last
-          // chunk shorter than K.
-          auto chunk_body = [&](auto full_tag) {
-            constexpr bool FULL = decltype(full_tag)::value;
-            // recompute the chunk: s_{t-1}, g_t and e*sin for every step
-            float SP[K][NPL], G[K][NPL], ES[K][NPL];
+          // adjoint over the chunk, last step first.  Parameter gradients
+          // sum into chunk-local fp32 accumulators, then into float64.
+          // cpt: the tracking-state sum of a slot decided at run time
+          float cpa[NPL], cpb[NPL], cpt[NPL];
 #pragma unroll
-            for (int m = 0; m < K; ++m) {
-              if (FULL || m < kcnt) {
-                const int row = m0 + m + 1;
-                const float dt = sCh[row][cl].x;
-                const float hd = sCh[row][cl].y;
+          for (int j = 0; j < NPL; ++j) {
+            cpa[j] = 0.f;
+            cpb[j] = 0.f;
+            cpt[j] = 0.f;
+          }
 #pragma unroll
-                for (int j = 0; j < NPL; ++j) {
-                  float es;
-                  const float g = gate_of<S, GK, true>(j, s, p.NR, has_imag, dt, gp.pah[j],
-                                                       gp.wh[j], sTab, es);
-                  const float hb = fmul(hd, sB[row][s * NPL + j]);
-                  const float sm = hc[j] + hbp[j];
-                  SP[m][j] = sm;
-                  G[m][j] = g;
-                  ES[m][j] = es;
-                  hc[j] = ffma(g, sm, hb);
-                  hbp[j] = hb;
+          for (int m = K - 1; m >= 0; --m) {
+            if (FULL || m < kcnt) {
+              const float4 chv = sCh[SL][m + 1][cl];
+              const float dt = chv.x, hd = chv.y, uu = chv.z, dy = chv.w;
+              float ddA = 0.f, ddB = 0.f, sBc = 0.f;
+#pragma unroll
+              for (int j = 0; j < NPL; ++j) {
+                const float Bv = sB[SL][m + 1][s * NPL + j];
+                const float Cv = sC[SL][m + 1][s * NPL + j];
+                const float g = G[m][j];
+                const float hb = fmul(hd, Bv);
+                const float ht = ffma(g, SP[m][j], hb);
+                const float q = ffma(dy, Cv, gq[j]);
+                const float dhb = q + gr[j];
+                sBc = ffma(dhb, Bv, sBc);
+                const float dg = fmul(q, SP[m][j]);
+                if (j >= GK::kTJ) {  // tracking in every lane
+                  cpa[j] = cpa[j] + dg;
+                } else {
+                  // rotational (for a slot decided at run time, a tracking
+                  // lane has pam = wh = es = 0 and sums dg into cpt)
+                  const float t1 = fmul(dg, g);
+                  const float t2 = fmul(dg, ES[m][j]);
+                  cpa[j] = ffma(t1, dt, cpa[j]);
+                  cpb[j] = ffma(t2, dt, cpb[j]);
+                  if (j >= GK::kRJ) cpt[j] = cpt[j] + dg;
+                  ddA = ffma(j < GK::kRJ ? gp.pah[j] : pam[j], t1, ddA);  // Ar log2(e) dg g
+                  ddB = ffma(gp.wh[j], t2, ddB);                          // Ai 16/(2 pi) dg e sin
                 }
+                gq[j] = fmul(g, q);
+                gr[j] = gq[j];
+                // every lane of the row holds the row's total for its slice
+                // s, so the lanes sharing s store the same value
+                sRed[m % KR][0][wrow][s * NPL + j] = reduce_row<S>(fmul(dhb, hd));
+                sRed[m % KR][1][wrow][s * NPL + j] = reduce_row<S>(fmul(dy, ht));
               }
+              ddA = reduce_states<S>(ddA);
+              ddB = reduce_states<S>(ddB);
+              sBc = reduce_states<S>(sBc);
+              // the channel's S lanes hold identical totals and store the same value
+              const float ddt = ffma(kLn2, ddA, -fmul(kPi8, ddB)) + fmul(0.5f * uu, sBc);
+              const float dut = fmul(0.5f * dt, sBc);
+              sDD[m][cl] = make_float2(ddt, dut);
             }
-            // adjoint over the chunk, last step first.  Parameter gradients
-            // sum into chunk-local fp32 accumulators, then into float64.
-            float cpa[NPL], cpb[NPL];
+            if (m % KR == 0) {
+              // the inputs of chunk ch-1 into the other slot
+              if (m == 0 && ch >= 1) stage_store(std::integral_constant<int, 1 - SL>{});
+              // fold the 16 row partials of steps [m, m + KR) into this
+              // tile's global dB / dC partials
+              __syncthreads();
 #pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-              cpa[j] = 0.f;
-              cpb[j] = 0.f;
-            }
-#pragma unroll
-            for (int m = K - 1; m >= 0; --m) {
-              if (FULL || m < kcnt) {
-                const int row = m0 + m + 1;
-                const float4 ch = sCh[row][cl];
-                const float dt = ch.x, hd = ch.y, uu = ch.z, dy = ch.w;
-                float ddA = 0.f, ddB = 0.f, sBc = 0.f;
-#pragma unroll
-                for (int j = 0; j < NPL; ++j) {
-                  const float Bv = sB[row][s * NPL + j];
-                  const float Cv = sC[row][s * NPL + j];
-                  const float g = G[m][j];
-                  const float hb = fmul(hd, Bv);
-                  const float ht = ffma(g, SP[m][j], hb);
-                  const float q = ffma(dy, Cv, gq[j]);
-                  const float dhb = q + gr[j];
-                  sBc = ffma(dhb, Bv, sBc);
-                  const float dg = fmul(q, SP[m][j]);
-                  if (is_rot<S, GK>(j, s, p.NR)) {
-                    const float t1 = fmul(dg, g);
-                    const float t2 = fmul(dg, ES[m][j]);
-                    cpa[j] = ffma(t1, dt, cpa[j]);
-                    cpb[j] = ffma(t2, dt, cpb[j]);
-                    ddA = ffma(gp.pah[j], t1, ddA);  // Ar log2(e) dg g
-                    ddB = ffma(gp.wh[j], t2, ddB);   // Ai 16/(2 pi) dg e sin
-                  } else {
-                    cpa[j] = cpa[j] + dg;
-                  }
-                  gq[j] = fmul(g, q);
-                  gr[j] = gq[j];
-                  const float xB = reduce_row<S>(fmul(dhb, hd));
-                  const float xC = reduce_row<S>(fmul(dy, ht));
-                  if (row_leader) {
-                    sRed[m % KR][0][wrow][s * NPL + j] = xB;
-                    sRed[m % KR][1][wrow][s * NPL + j] = xC;
-                  }
-                }
-                ddA = reduce_states<S>(ddA);
-                ddB = reduce_states<S>(ddB);
-                sBc = reduce_states<S>(sBc);
-                if (s == 0) {
-                  const float ddt = ffma(kLn2, ddA, -fmul(kPi8, ddB)) + fmul(0.5f * uu, sBc);
-                  const float dut = fmul(0.5f * dt, sBc);
-                  sDD[m0 + m][cl] = make_float2(ddt, dut);
-                }
-              }
-              if (m % KR == 0) {
-                // fold the 16 row partials of steps [m, m + KR) into this
-                // tile's global dB / dC partials
-                __syncthreads();
-                for (int e = tid; e < KR * 2 * p.N; e += kThreads) {
-                  const int rr = e / (2 * p.N);
+              for (int k = 0; k < FPT; ++k) {
+                const int e = tid + k * kThreads;
+                float* dst = fold_dst(e, b, dir, i0, m, kcnt);
+                if (dst != nullptr) {
                   const int rem = e % (2 * p.N);
                   const int which = rem / p.N, n = rem % p.N;
-                  if (m + rr < kcnt) {
-                    const int k = (n % S) * NPL + n / S;
-                    float v = sRed[rr][which][0][k];
+                  const int kk = (n % S) * NPL + n / S;
+                  float v = sRed[e / (2 * p.N)][which][0][kk];
 #pragma unroll
-                    for (int w = 1; w < NRW; ++w) v = v + sRed[rr][which][w][k];
-                    const int i = i0 + m0 + m + rr;
-                    const int t = dir ? (L - 1 - i) : i;
-                    float* dst = io.part_bc +
-                                 (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
-                                 (int64_t)t * p.N + n;
-                    if (dir == 0)
-                      *dst = v;
-                    else
-                      *dst = *dst + v;
+                  for (int w = 1; w < NRW; ++w) v = v + sRed[e / (2 * p.N)][which][w][kk];
+                  *dst = dir == 0 ? v : prev[m / KR][k] + v;
+                }
+              }
+              if (m == 0) {
+                // the chunk's (d_delta, d_u), channel-contiguous
+#pragma unroll
+                for (int k = 0; k < DPT; ++k) {
+                  const int e = tid + k * kThreads;
+                  const int64_t idx = dd_index(e, b, dir, i0, kcnt);
+                  if (idx >= 0) {
+                    const float2 v = sDD[e / CB][e % CB];
+                    io.d_delta[idx] = dir == 0 ? v.x : pdd[k][0] + v.x;
+                    io.d_u[idx] = dir == 0 ? v.y : pdd[k][1] + v.y;
                   }
                 }
-                __syncthreads();
               }
-            }
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) {
-              dpa[j] += (double)cpa[j];
-              dpb[j] += (double)cpb[j];
-            }
-          };
-          if (kcnt == K)
-            chunk_body(std::true_type{});
-          else
-            chunk_body(std::false_type{});
-        }
-        // the block's (d_delta, d_u) rows, written channel-contiguous
-        for (int e = tid; e < cnt * CB; e += kThreads) {
-          const int r = e / CB, ci = e % CB;
-          const int c2 = tile * CB + ci;
-          if (c2 < p.D) {
-            const int i = i0 + r;
-            const int t = dir ? (L - 1 - i) : i;
-            const float2 v = sDD[r][ci];
-            const int64_t idx = ((int64_t)b * L + t) * p.D + c2;
-            if (dir == 0) {
-              io.d_delta[idx] = v.x;
-              io.d_u[idx] = v.y;
-            } else {
-              io.d_delta[idx] = io.d_delta[idx] + v.x;
-              io.d_u[idx] = io.d_u[idx] + v.y;
+              __syncthreads();
             }
           }
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            const float a = (j >= GK::kRJ && j < GK::kTJ && !is_rot<S, GK>(j, s, p.NR)) ? cpt[j]
+                                                                                        : cpa[j];
+            sPar[0][j][tid] += (double)a;
+            if (j < GK::kTJ) sPar[1][j][tid] += (double)cpb[j];
+          }
+        };
+        if (kcnt == K) {
+          if (ch % 2 == 0)
+            chunk_body(std::true_type{}, Slot0{});
+          else
+            chunk_body(std::true_type{}, Slot1{});
+        } else {
+          if (ch % 2 == 0)
+            chunk_body(std::false_type{}, Slot0{});
+          else
+            chunk_body(std::false_type{}, Slot1{});
         }
       }
       // after the sweep gq = g_0 q_0: the gradient of the initial state, since
@@ -322,8 +440,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       const int n = j * S + s;
       if (n < p.N) {
         const int64_t base = ((int64_t)bgi * 2) * p.D * p.N;
-        io.part_par[base + (int64_t)c * p.N + n] = dpa[j];
-        io.part_par[base + (int64_t)p.D * p.N + (int64_t)c * p.N + n] = dpb[j];
+        io.part_par[base + (int64_t)c * p.N + n] = sPar[0][j][tid];
+        io.part_par[base + (int64_t)p.D * p.N + (int64_t)c * p.N + n] = sPar[1][j][tid];
       }
     }
   }
@@ -369,12 +487,13 @@ static hipError_t launch_bwd_t(const ScanParams& p, const BwdIO& io, hipStream_t
   return hipGetLastError();
 }
 
-hipError_t launch_scan_bwd(int S, int NPL, bool spec, const ScanParams& p, const BwdIO& io,
+hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const BwdIO& io,
                            hipStream_t st) {
-#define RP_CASE(SS, NN)                                                          \
-  if (S == SS && NN == NPL)                                                      \
-    return spec ? launch_bwd_t<SS, NN, GateKind<NN - 1, 1>>(p, io, st)           \
-                : launch_bwd_t<SS, NN, GateKind<0, 2>>(p, io, st);
+#define RP_CASE(SS, NN)                                                              \
+  if (S == SS && NN == NPL)                                                          \
+    return with_gate_kind<NN>(gk, [&](auto g) {                                      \
+      return launch_bwd_t<SS, NN, decltype(g)>(p, io, st);                           \
+    });
   RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
   return hipErrorInvalidValue;

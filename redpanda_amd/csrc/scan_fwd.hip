@@ -130,12 +130,13 @@ static hipError_t launch_fwd_t(const ScanParams& p, const FwdOut& o, hipStream_t
   return hipGetLastError();
 }
 
-hipError_t launch_scan_fwd(int S, int NPL, bool spec, const ScanParams& p, const FwdOut& o,
+hipError_t launch_scan_fwd(int S, int NPL, int gk, const ScanParams& p, const FwdOut& o,
                            hipStream_t st) {
-#define RP_CASE(SS, NN)                                                          \
-  if (S == SS && NN == NPL)                                                      \
-    return spec ? launch_fwd_t<SS, NN, GateKind<NN - 1, 1>>(p, o, st)            \
-                : launch_fwd_t<SS, NN, GateKind<0, 2>>(p, o, st);
+#define RP_CASE(SS, NN)                                                              \
+  if (S == SS && NN == NPL)                                                          \
+    return with_gate_kind<NN>(gk, [&](auto g) {                                      \
+      return launch_fwd_t<SS, NN, decltype(g)>(p, o, st);                            \
+    });
   RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
   return hipErrorInvalidValue;

@@ -251,27 +251,29 @@ static hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
 }
 
 template <int S, int NPL>
-static hipError_t launch_step_tile(bool spec, const StepParams& p, hipStream_t st) {
+static hipError_t launch_step_tile(int gk, const StepParams& p, hipStream_t st) {
   if constexpr (S * NPL <= 40) {
-    return spec ? launch_step_tile_t<S, NPL, GateKind<NPL - 1, 1>>(p, st)
-                : launch_step_tile_t<S, NPL, GateKind<0, 2>>(p, st);
+    return with_gate_kind<NPL>(gk, [&](auto g) {
+      return launch_step_tile_t<S, NPL, decltype(g)>(p, st);
+    });
   } else {
     return hipErrorInvalidValue;
   }
 }
 
-hipError_t launch_step(int S, int NPL, bool spec, bool tile, const StepParams& p, hipStream_t st) {
+hipError_t launch_step(int S, int NPL, int gk, bool tile, const StepParams& p, hipStream_t st) {
   if (tile) {
 #define RP_CASE(SS, NN) \
-    if (S == SS && NN == NPL) return launch_step_tile<SS, NN>(spec, p, st);
+    if (S == SS && NN == NPL) return launch_step_tile<SS, NN>(gk, p, st);
     RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
     return hipErrorInvalidValue;
   }
 #define RP_CASE(SS, NN)                                                    \
   if (S == SS && NN == NPL)                                                \
-    return spec ? launch_step_t<SS, NN, GateKind<NN - 1, 1>>(p, st)        \
-                : launch_step_t<SS, NN, GateKind<0, 2>>(p, st);
+    return with_gate_kind<NN>(gk, [&](auto g) {                            \
+      return launch_step_t<SS, NN, decltype(g)>(p, st);                    \
+    });
   RP_FOR_EACH_SHAPE(RP_CASE)
 #undef RP_CASE
   return hipErrorInvalidValue;

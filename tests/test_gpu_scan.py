@@ -173,6 +173,16 @@ def test_edge_lengths(gpu_lib, L):
     compare(c, False, f"L={L}")
 
 
+def test_empty_sequence(gpu_lib):
+    """L = 0: nothing to scan, and every parameter gradient is zero."""
+    c = make_case(99, B=2, L=0, D=40, NR=8, NT=4)
+    for bidir in (False, True):
+        y, g = hip_run(c, bidir)
+        assert y.shape == (2, 0, 40)
+        for k in ("Ar", "Ai", "Tk"):
+            assert torch.count_nonzero(g[k]).item() == 0, k
+
+
 @pytest.mark.parametrize("D", [1, 16, 63, 64, 65, 200])
 def test_channel_counts(gpu_lib, D):
     c = make_case(200 + D, B=2, L=20, D=D, NR=12, NT=4)
