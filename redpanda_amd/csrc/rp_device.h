@@ -18,11 +18,12 @@
 // relative error per step, so a gate close to 1, which carries state over
 // M ~ 1/(1-g) steps, turns it into a relative drift of ~M x bias in the state
 // and in every gradient that sums over steps.  The rotational cos / sin are
-// therefore evaluated to ~1 ulp without bias: the angle in 1/16 revolutions
-// is reduced exactly to a table index plus a remainder |x| <= pi/16, where
-// short Taylor polynomials are accurate to < 3e-9.  (Rounding Ar*log2(e)
-// and 16*Ai/(2 pi) once per state is harmless by contrast: its error
-// scales with dt*A, so it stays ~1 ulp of the state over any memory length.)
+// therefore evaluated to ~1 ulp without bias: the angle in 1/256 revolutions
+// is reduced exactly to a table index plus a remainder |x| <= pi/256, where
+// cos x - 1 = -x^2/2 and sin x = x - x^3/6 are accurate to 1e-9 absolute
+// (a bias below 0.01 ulp).  (Rounding Ar*log2(e) and 256*Ai/(2 pi) once per
+// state is harmless by contrast: its error scales with dt*A, so it stays
+// ~1 ulp of the state over any memory length.)
 // The forward, the step and the backward's recompute share the code, so the
 // backward recomputes exactly the gates the forward used.
 #pragma once
@@ -32,6 +33,7 @@
 
 #include "redpanda_hip.h"
 #include "rp_launch.h"
+#include "rp_sincos_table.h"
 
 namespace rp {
 
@@ -74,35 +76,21 @@ __device__ __forceinline__ float ffma(float a, float b, float c) { return __buil
 // exp2 on the transcendental unit (v_exp_f32).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// cos / sin of 2 pi k / 16, k = 0..15 (filled into LDS once per workgroup).
-__device__ __forceinline__ void sincos_table_entry(int k, float& c, float& s) {
-  constexpr float kC1 = 0.923879532511286756f, kC2 = 0.707106781186547524f,
-                  kC3 = 0.382683432365089772f;
-  const float cq[4] = {1.f, kC1, kC2, kC3};  // cos of 0, 1/16, 2/16, 3/16 rev
-  const int q = (k >> 2) & 3, r = k & 3;
-  const float c0 = cq[r];
-  const float s0 = (r == 0) ? 0.f : cq[(4 - r) & 3];
-  c = (q == 0) ? c0 : (q == 1) ? -s0 : (q == 2) ? -c0 : s0;
-  s = (q == 0) ? s0 : (q == 1) ? c0 : (q == 2) ? -s0 : -c0;
-}
-
+// The cos / sin table (kTab entries of 2 pi k / kTab) copied into LDS once
+// per workgroup; read after the workgroup's next barrier.
 __device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
-  if (tid < 16) {
-    float c, s;
-    sincos_table_entry(tid, c, s);
-    tab[tid] = make_float2(c, s);
-  }
+  for (int k = tid; k < kTab; k += kThreads) tab[k] = kSinCosTable[k];
 }
 
 // Per-state gate parameters held in registers: pah = fl(A_real log2(e)) and
-// wh = fl(16 A_imag / (2 pi)) (the angle rate in 1/16 revolutions) for
+// wh = fl(256 A_imag / (2 pi)) (the angle rate in 1/256 revolutions) for
 // rotational states; pah = tanh(theta) for tracking states; zeros for pad.
 __device__ __forceinline__ void load_gate_params(const float* Ar, const float* Ai, const float* Tk,
                                                  int c, int n, int N, int NR, int NT, bool valid,
                                                  float& pah, float& wh) {
   // x * K with K split as kHi + kLo: one rounding of the extended product
   constexpr float kL2eHi = 1.4426950216293335f, kL2eLo = 1.925963033500011e-08f;  // log2(e)
-  constexpr float kW16Hi = 2.5464789867401123f, kW16Lo = 1.0273021189277642e-07f;   // 16/(2 pi)
+  constexpr float kWHi = 40.7436637878418f, kWLo = 1.6436833902844228e-06f;  // 256/(2 pi)
   pah = 0.f;
   wh = 0.f;
   if (!valid) return;
@@ -111,21 +99,19 @@ __device__ __forceinline__ void load_gate_params(const float* Ar, const float* A
     pah = ffma(a, kL2eHi, fmul(a, kL2eLo));
     if (Ai != nullptr) {
       const float w = Ai[(int64_t)c * NR + n];
-      wh = ffma(w, kW16Hi, fmul(w, kW16Lo));
+      wh = ffma(w, kWHi, fmul(w, kWLo));
     }
   } else if (n < N) {
     pah = Tk[(int64_t)c * NT + (n - NR)];
   }
 }
 
-constexpr float kPi8 = 0.39269908169872415481f;  // pi / 8: radians per table step
-constexpr float kRint = 12582912.f;               // 1.5 * 2^23: x + kRint rounds x to an integer
-// cos(pi/8 r) - 1 = r^2 (kC2 + r^2 (kC4 + r^2 kC6)),  sin(pi/8 r) = r (kS1 + r^2 (kS3 + r^2 kS5))
-// for |r| <= 1/2 (Taylor, truncation < 6e-11 and < 3e-9)
-constexpr float kC2 = -0.07710628438351061f, kC4 = 0.0009908965152384687f,
-                kC6 = -5.093623233240468e-06f;
-constexpr float kS1 = 0.39269908169872414f, kS3 = -0.010093189023535096f,
-                kS5 = 7.78248303185225e-05f;
+constexpr float kRadPerStep = 0.02454369328916073f;  // 2 pi / 256: radians per table step
+constexpr float kRint = 12582912.f;  // 1.5 * 2^23: x + kRint rounds x to an integer
+// With a = 2 pi / 256 and |r| <= 1/2:  cos(a r) - 1 = kC2 r^2  (truncation
+// < 9.5e-10),  sin(a r) = r (kS1 + kS3 r^2)  (truncation < 2.4e-12)
+constexpr float kC2 = -0.0003011964145116508f;
+constexpr float kS1 = 0.02454369328916073f, kS3 = -2.464157432768843e-06f;
 
 // How a kernel instantiation knows the rotational / tracking split:
 //   RJ   leading state slots j < RJ are rotational in every lane (compile
@@ -143,8 +129,8 @@ struct GateKind {
   static constexpr int kTJ = TJ;
 };
 
-// Rotational gate g = 2^(dt pah) cos(pi/8 dt wh); with WITH_SIN also
-// es = 2^(dt pah) sin(pi/8 dt wh) for the backward.  The angle dt*wh is split
+// Rotational gate g = 2^(dt pah) cos(a dt wh), a = 2 pi / 256; with WITH_SIN
+// also es = 2^(dt pah) sin(a dt wh) for the backward.  The angle dt*wh is split
 // exactly into an integer k (the table index, by the round-to-integer
 // addition) and a remainder |r| <= 1/2.  The cos path is the same code in
 // both instantiations, so g is bitwise the same.
@@ -154,7 +140,7 @@ struct GateKind {
 // them (rot_gate_issue, then rot_gate_finish); rot_gate is the two in a row.
 struct GatePart {
   float e;    // 2^(dt pah)
-  float r;    // angle remainder, |r| <= 1/2 (1/16 revolutions)
+  float r;    // angle remainder, |r| <= 1/2 (table steps)
   float2 cs;  // cos, sin of the table angle
 };
 
@@ -171,7 +157,7 @@ __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh
   const float t = w + kRint;
   const float kf = t - kRint;  // rint(w), exact
   g.r = w - kf;                // exact
-  g.cs = tab[__float_as_int(t) & 15];
+  g.cs = tab[__float_as_int(t) & (kTab - 1)];
   return g;
 }
 
@@ -183,8 +169,8 @@ __device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag, f
   }
   const float r = g.r;
   const float r2 = fmul(r, r);
-  const float cm1 = fmul(r2, ffma(r2, ffma(r2, kC6, kC4), kC2));  // cos - 1
-  const float sx = fmul(r, ffma(r2, ffma(r2, kS5, kS3), kS1));    // sin
+  const float cm1 = fmul(r2, kC2);                 // cos - 1
+  const float sx = fmul(r, ffma(r2, kS3, kS1));    // sin
   const float cv = ffma(-g.cs.y, sx, ffma(g.cs.x, cm1, g.cs.x));
   if (WITH_SIN) {
     const float sv = ffma(g.cs.x, sx, ffma(g.cs.y, cm1, g.cs.y));

@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float sC[2][KS][NP];
   __shared__ float sRed[KR][2][NRW][NP];  // per-row channel sums of dB, dC
   __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
-  __shared__ float2 sTab[16];             // cos, sin of 2 pi k / 16
+  __shared__ float2 sTab[kTab];             // cos, sin of 2 pi k / kTab
   // per-thread float64 sums of the parameter gradients over the batch group
   // (dA_real or dtrack, dA_imag), kept in LDS to spare registers
   __shared__ double sPar[2][NPL][kThreads];
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   cpb[j] = ffma(t2, dt, cpb[j]);
                   if (j >= GK::kRJ) cpt[j] = cpt[j] + dg;
                   ddA = ffma(j < GK::kRJ ? gp.pah[j] : pam[j], t1, ddA);  // Ar log2(e) dg g
-                  ddB = ffma(gp.wh[j], t2, ddB);                          // Ai 16/(2 pi) dg e sin
+                  ddB = ffma(gp.wh[j], t2, ddB);                          // Ai 256/(2 pi) dg e sin
                 }
                 gq[j] = fmul(g, q);
                 gr[j] = gq[j];
@@ -358,7 +358,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               ddB = reduce_states<S>(ddB);
               sBc = reduce_states<S>(sBc);
               // the channel's S lanes hold identical totals and store the same value
-              const float ddt = ffma(kLn2, ddA, -fmul(kPi8, ddB)) + fmul(0.5f * uu, sBc);
+              const float ddt = ffma(kLn2, ddA, -fmul(kRadPerStep, ddB)) + fmul(0.5f * uu, sBc);
               const float dut = fmul(0.5f * dt, sBc);
               sDD[m][cl] = make_float2(ddt, dut);
             }

@@ -25,7 +25,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   __shared__ float2 sDH[TB][CB];   // (dt, (dt*u)/2) per step and channel
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
-  __shared__ float2 sTab[16];      // cos, sin of 2 pi k / 16
+  __shared__ float2 sTab[kTab];      // cos, sin of 2 pi k / kTab
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;

@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   const bool cvalid = c < p.D;
   const bool has_imag = p.Ai != nullptr;
 
-  __shared__ float2 sTab[16];  // cos, sin of 2 pi k / 16
+  __shared__ float2 sTab[kTab];  // cos, sin of 2 pi k / kTab
   fill_sincos_table(sTab, tid);
   GateRegs<NPL> gp;
   float h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
   constexpr int TCH = kStepTile;
-  __shared__ float2 sTab[16];           // cos, sin of 2 pi k / 16
+  __shared__ float2 sTab[kTab];           // cos, sin of 2 pi k / kTab
   __shared__ float2 sGate[NP][TCH];     // (pah, wh) of every channel's states
   __shared__ float sBC[2][2 * NP];       // B, C rows of the current / next rollout
   const int tid = threadIdx.x;
