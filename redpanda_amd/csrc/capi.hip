@@ -52,7 +52,7 @@ int step_ri_override() {
   static int v = [] {
     const char* s = getenv("RP_STEP_RI");
     const int x = s ? atoi(s) : 0;
-    return (x >= 1 && x <= 64) ? x : 0;
+    return (x >= 1 && x <= rp::kStepRiMax) ? x : 0;
   }();
   return v;
 }
@@ -396,16 +396,17 @@ int rp_step(const rp_step_args* a, void* stream) {
                     (a->h_in == nullptr || (aligned(a->h_in, 16) && aligned(a->beta_in, 16)));
   if (tile) {
     p.ctiles = (int)((a->D + rp::kStepTile - 1) / rp::kStepTile);
-    // rollouts per workgroup: several amortise loading the gate parameters,
-    // while the grid keeps a few thousand workgroups
+    // rollouts per workgroup: a few amortise the workgroup's prologue (gate
+    // parameters, B / C rows) while keeping many workgroups in flight;
+    // measured at 4096 rollouts x 1024 channels, d_state 20: 4 per workgroup
+    // (4096 workgroups) beat 1..3 and 6..32
     int64_t ri = step_ri_override();
     if (ri == 0) {
-      // measured at 4096 rollouts x 1024 channels: 32 rollouts per
-      // workgroup (512 workgroups) beat 4..16 and 64
-      ri = (a->R * (int64_t)p.ctiles) / 512;
+      ri = (a->R * (int64_t)p.ctiles) / 2048;
       if (ri < 1) ri = 1;
-      if (ri > 32) ri = 32;
+      if (ri > 4) ri = 4;
     }
+    if (ri > rp::kStepRiMax) return fail(RP_ERR_UNSUPPORTED, "step: rollouts per workgroup");
     p.ri = (int)ri;
     p.rgroups = (int)((a->R + ri - 1) / ri);
     if ((int64_t)p.ctiles * p.rgroups > kI32Max)

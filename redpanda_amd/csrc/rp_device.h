@@ -85,25 +85,41 @@ __device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
 // Per-state gate parameters held in registers: pah = fl(A_real log2(e)) and
 // wh = fl(256 A_imag / (2 pi)) (the angle rate in 1/256 revolutions) for
 // rotational states; pah = tanh(theta) for tracking states; zeros for pad.
-__device__ __forceinline__ void load_gate_params(const float* Ar, const float* Ai, const float* Tk,
-                                                 int c, int n, int N, int NR, int NT, bool valid,
-                                                 float& pah, float& wh) {
+// In two phases, so that a caller issues the loads of all its states before
+// the first value is needed: gate_param_load fetches without lane-divergent
+// control flow (every lane loads from a valid address: Ar is non-null when
+// NR > 0 and Tk when NT > 0), gate_param_finish selects and converts.
+struct GateRaw {
+  float ar, ai, tk;
+};
+
+__device__ __forceinline__ GateRaw gate_param_load(const float* Ar, const float* Ai,
+                                                   const float* Tk, int c, int n, int N, int NR,
+                                                   int NT, bool valid) {
+  const bool rot = valid && n < NR;
+  const bool trk = valid && n >= NR && n < N;
+  const int64_t ir = rot ? (int64_t)c * NR + n : 0;
+  const int64_t it = trk ? (int64_t)c * NT + (n - NR) : 0;
+  GateRaw g{0.f, 0.f, 0.f};
+  if (NR > 0) {
+    g.ar = Ar[ir];
+    if (Ai != nullptr) g.ai = Ai[ir];
+  }
+  if (NT > 0) g.tk = Tk[it];
+  return g;
+}
+
+__device__ __forceinline__ void gate_param_finish(int n, int N, int NR, bool valid,
+                                                  const GateRaw& g, float& pah, float& wh) {
   // x * K with K split as kHi + kLo: one rounding of the extended product
   constexpr float kL2eHi = 1.4426950216293335f, kL2eLo = 1.925963033500011e-08f;  // log2(e)
   constexpr float kWHi = 40.7436637878418f, kWLo = 1.6436833902844228e-06f;  // 256/(2 pi)
-  pah = 0.f;
-  wh = 0.f;
-  if (!valid) return;
-  if (n < NR) {
-    const float a = Ar[(int64_t)c * NR + n];
-    pah = ffma(a, kL2eHi, fmul(a, kL2eLo));
-    if (Ai != nullptr) {
-      const float w = Ai[(int64_t)c * NR + n];
-      wh = ffma(w, kWHi, fmul(w, kWLo));
-    }
-  } else if (n < N) {
-    pah = Tk[(int64_t)c * NT + (n - NR)];
-  }
+  const bool rot = valid && n < NR;
+  const bool trk = valid && n >= NR && n < N;
+  const float pr = ffma(g.ar, kL2eHi, fmul(g.ar, kL2eLo));
+  const float wr = ffma(g.ai, kWHi, fmul(g.ai, kWLo));
+  pah = rot ? pr : (trk ? g.tk : 0.f);
+  wh = rot ? wr : 0.f;
 }
 
 constexpr float kRadPerStep = 0.02454369328916073f;  // 2 pi / 256: radians per table step
@@ -267,9 +283,11 @@ template <int S, int NPL>
 __device__ __forceinline__ void load_gate_regs(GateRegs<NPL>& gp, const float* Ar, const float* Ai,
                                                const float* Tk, int c, int s, int N, int NR,
                                                int NT, bool valid) {
+  GateRaw g[NPL];
 #pragma unroll
-  for (int j = 0; j < NPL; ++j)
-    load_gate_params(Ar, Ai, Tk, c, j * S + s, N, NR, NT, valid, gp.pah[j], gp.wh[j]);
+  for (int j = 0; j < NPL; ++j) g[j] = gate_param_load(Ar, Ai, Tk, c, j * S + s, N, NR, NT, valid);
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) gate_param_finish(j * S + s, N, NR, valid, g[j], gp.pah[j], gp.wh[j]);
 }
 
 // One recurrence step for the lane's NPL states; returns the lane's partial

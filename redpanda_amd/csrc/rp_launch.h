@@ -80,8 +80,10 @@ struct StepParams {
   int rgroups;  // tile kernel: ceil(R / ri)
 };
 
-// Channels (one per thread) of the step tile kernel's workgroup.
+// Channels (one per thread) of the step tile kernel's workgroup, and the
+// most rollouts one of its workgroups walks.
 constexpr int kStepTile = kThreads;
+constexpr int kStepRiMax = 16;
 
 // Chosen lane split for a state dimension N: S lanes per channel holding NPL
 // states each.  Returns false when N is beyond the compiled shapes.

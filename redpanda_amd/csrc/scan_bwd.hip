@@ -79,9 +79,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   const bool has_imag = p.Ai != nullptr;
   const int L = p.L;
 
-  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
-  GateRegs<NPL> gp;
+  GateRegs<NPL> gp;  // loads issued first, so the table copy overlaps them
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
+  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
   // pam: the coefficient of the ddt sum over rotational states, zero for a
   // tracking state (only read for slots whose kind is decided at run time)
   float pam[NPL];

@@ -37,9 +37,9 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   const bool has_imag = p.Ai != nullptr;
   const int L = p.L;
 
-  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
-  GateRegs<NPL> gp;
+  GateRegs<NPL> gp;  // loads issued first, so the table copy overlaps them
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
+  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
 
   const int nblk = (L + TB - 1) / TB;
   for (int dir = 0; dir < p.ndir; ++dir) {

@@ -8,10 +8,13 @@
 //
 // Two kernels, bitwise the same as each other and as the scan:
 //   * step_tile_kernel (the rollout path: d_state == S*NPL, a multiple of 4,
-//     <= 40): one thread per channel holding all of the channel's states,
-//     read and written as aligned 16-byte vectors; a workgroup owns 256
-//     channels and walks a group of rollouts, keeping the gate parameters in
-//     registers.  B and C are wave-uniform.
+//     <= 40): a workgroup owns 256 channels and walks a few rollouts.  Per
+//     rollout, the (256 channels x d_state) blocks of h and beta move with
+//     coalesced streaming 16-byte loads and stores through LDS, where one
+//     thread per channel updates its states; the gate parameters stay in
+//     registers and the B / C rows in LDS for all the workgroup's rollouts.
+//     (Moving each channel's 80 contiguous bytes per thread instead costs
+//     ~15% of the bandwidth.)
 //   * step_kernel: the scan's lane layout (S lanes per channel), for any
 //     other shape.
 // Both run the scan's per-state arithmetic (gate_of / fwd_update in
@@ -21,6 +24,8 @@
 // matches the scan bit for bit.  beta' is stored as 2 * ((dt*u)/2 * B) =
 // (dt*u) * B exactly, the association of the reference's dBu_t
 // (engine/mamba.py:481).
+
+#include <type_traits>
 
 #include "rp_device.h"
 #include "rp_launch.h"
@@ -120,133 +125,165 @@ __device__ __forceinline__ float tree_sum(const float (&v)[S]) {
   }
 }
 
-template <int S, int NPL, class GK>
+// Streaming 16-byte loads and stores that bypass cache retention (the state
+// is read once and written once per launch).
+__device__ __forceinline__ float4 load_stream(const float4* p) {
+  float4 v;
+  v.x = __builtin_nontemporal_load(&p->x);
+  v.y = __builtin_nontemporal_load(&p->y);
+  v.z = __builtin_nontemporal_load(&p->z);
+  v.w = __builtin_nontemporal_load(&p->w);
+  return v;
+}
+__device__ __forceinline__ void store_stream(float4* p, float4 v) {
+  __builtin_nontemporal_store(v.x, &p->x);
+  __builtin_nontemporal_store(v.y, &p->y);
+  __builtin_nontemporal_store(v.z, &p->z);
+  __builtin_nontemporal_store(v.w, &p->w);
+}
+
+// FULLD: D is a multiple of the workgroup's 256 channels (no channel guard).
+template <int S, int NPL, class GK, bool FULLD>
 __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
   constexpr int TCH = kStepTile;
   __shared__ float2 sTab[kTab];           // cos, sin of 2 pi k / kTab
-  __shared__ float2 sGate[NP][TCH];     // (pah, wh) of every channel's states
-  __shared__ float sBC[2][2 * NP];       // B, C rows of the current / next rollout
+  __shared__ float sBC[kStepRiMax][2 * NP];  // B, C rows of the workgroup's rollouts
+  // the (h, beta) block of one rollout: TCH channels x NP states each, as in
+  // memory ([channel][state]), so float4 k holds channel k / NV
+  __shared__ float4 sH[TCH * NV], sBt[TCH * NV];
   const int tid = threadIdx.x;
   const int tile = blockIdx.x % p.ctiles, rg = blockIdx.x / p.ctiles;
-  const int c = tile * TCH + tid;
-  const bool cvalid = c < p.D;
+  const int c0 = tile * TCH;
+  const int c = c0 + tid;
+  const bool cvalid = FULLD || c < p.D;
+  const int cld = cvalid ? c : p.D - 1;  // loads stay in bounds; only valid channels store
+  const int nvalid = FULLD ? TCH * NV : min(TCH, p.D - c0) * NV;  // float4s of the block
   const bool has_imag = p.Ai != nullptr;
   const int N = p.N;                    // N == NP (checked by the host)
-  fill_sincos_table(sTab, tid);
-  // gate parameters live in LDS (conflict-free [state][thread] layout), so
-  // the registers hold the rollout's states only
-#pragma unroll
-  for (int n = 0; n < NP; ++n) {
-    float a, w;
-    load_gate_params(p.Ar, p.Ai, p.Tk, c, n, N, p.NR, p.NT, cvalid, a, w);
-    sGate[n][tid] = make_float2(a, w);
-  }
-  const float dsk = cvalid ? p.Dskip[c] : 0.f;
-
   const int r_lo = rg * p.ri;
-  const int r_hi = min(p.R, r_lo + p.ri);
-  // Software pipeline over the workgroup's rollouts: everything rollout r+1
-  // needs (its state vectors, dt and u, and its B / C rows, staged through a
-  // double-buffered LDS row) is requested before rollout r is computed, so
-  // every wave keeps a rollout of loads in flight.  The channel's states are
-  // NP contiguous floats: NV aligned 16-byte vectors.
-  float4 hv[NV], bv[NV], hn[NV], bn[NV];
-  auto load_state = [&](int r, float4 (&h4)[NV], float4 (&b4)[NV]) {
-    const int64_t base = ((int64_t)r * p.D + c) * NP;
-    if (p.h_in != nullptr && cvalid) {
-      const float4* hi4 = reinterpret_cast<const float4*>(p.h_in + base);
-      const float4* bi4 = reinterpret_cast<const float4*>(p.beta_in + base);
+  const int nr = min(p.R, r_lo + p.ri) - r_lo;  // <= kStepRiMax (checked by the host)
+  // The prologue issues every load (B / C rows, gate parameters, D) before
+  // it stores anything, so their latencies overlap.  The B / C rows of all
+  // the workgroup's rollouts are staged once.
+  constexpr int BCPT = (kStepRiMax * 2 * NP + kThreads - 1) / kThreads;
+  float bc[BCPT];
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        h4[v] = hi4[v];
-        b4[v] = bi4[v];
+  for (int k = 0; k < BCPT; ++k) {
+    const int e = tid + k * kThreads;
+    const int rr = e / (2 * NP), q = e % (2 * NP);
+    const int64_t r = r_lo + rr;
+    bc[k] = 0.f;
+    if (e < nr * 2 * NP) bc[k] = q < NP ? p.Bc[r * p.bsr + q] : p.Cc[r * p.csr + (q - NP)];
+  }
+  // the channel's gate parameters stay in registers for all its rollouts
+  GateRaw graw[NP];
+#pragma unroll
+  for (int n = 0; n < NP; ++n) graw[n] = gate_param_load(p.Ar, p.Ai, p.Tk, cld, n, N, p.NR, p.NT, true);
+  const float dsk = p.Dskip[cld];
+  fill_sincos_table(sTab, tid);
+#pragma unroll
+  for (int k = 0; k < BCPT; ++k) {
+    const int e = tid + k * kThreads;
+    if (e < nr * 2 * NP) sBC[e / (2 * NP)][e % (2 * NP)] = bc[k];
+  }
+  float pah[NP], wh[NP];
+#pragma unroll
+  for (int n = 0; n < NP; ++n) gate_param_finish(n, N, p.NR, true, graw[n], pah[n], wh[n]);
+
+  // Per rollout: the block's (h, beta) arrive with coalesced streaming loads
+  // (thread t moves float4s t, t+256, ...) into LDS; each thread updates its
+  // channel's states there; coalesced streaming stores write the block back.
+  // Every input is in LDS or registers before the first store, so h_out and
+  // beta_out may alias h_in and beta_in.
+  for (int rr = 0; rr < nr; ++rr) {
+    const int64_t r = r_lo + rr;
+    const int64_t blk = (r * p.D + c0) * NV;  // float4 offset of the block
+    const float dt = p.delta[r * p.dsr + cld];
+    const float uu = p.u[r * p.usr + cld];
+    if (p.h_in != nullptr) {
+      const float4* hi4 = reinterpret_cast<const float4*>(p.h_in) + blk;
+      const float4* bi4 = reinterpret_cast<const float4*>(p.beta_in) + blk;
+      float4 hl[NV], bl[NV];
+#pragma unroll
+      for (int m = 0; m < NV; ++m) {
+        const int k = tid + m * TCH;
+        if (FULLD || k < nvalid) {
+          hl[m] = load_stream(hi4 + k);
+          bl[m] = load_stream(bi4 + k);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < NV; ++m) {
+        const int k = tid + m * TCH;
+        if (FULLD || k < nvalid) {
+          sH[k] = hl[m];
+          sBt[k] = bl[m];
+        }
       }
     } else {
 #pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        h4[v] = make_float4(0.f, 0.f, 0.f, 0.f);
-        b4[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int m = 0; m < NV; ++m) {
+        sH[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
+        sBt[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
-  };
-  // B / C of a rollout: thread t < 2*NP loads element t (B then C)
-  auto load_bc = [&](int r) -> float {
-    if (tid < 2 * NP) {
-      const int n = tid % NP;
-      return tid < NP ? p.Bc[(int64_t)r * p.bsr + n] : p.Cc[(int64_t)r * p.csr + n];
+    __syncthreads();  // the block (and, the first time, the table and B / C rows)
+    float4 h4[NV], b4[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      h4[v] = sH[tid * NV + v];
+      b4[v] = sBt[tid * NV + v];
     }
-    return 0.f;
-  };
-  auto load_du = [&](int r, float& d, float& u) {
-    d = cvalid ? p.delta[(int64_t)r * p.dsr + c] : 0.f;
-    u = cvalid ? p.u[(int64_t)r * p.usr + c] : 0.f;
-  };
-  float dtc = 0.f, uc = 0.f, dtn = 0.f, un = 0.f;
-  if (r_lo < r_hi) {
-    load_state(r_lo, hv, bv);
-    load_du(r_lo, dtc, uc);
-    const float bc0 = load_bc(r_lo);
-    if (tid < 2 * NP) sBC[0][tid] = bc0;
-  }
-  __syncthreads();  // the sin/cos table and the first B / C row
-  for (int r = r_lo; r < r_hi; ++r) {
-    const int buf = (r - r_lo) & 1;
-    float bcn = 0.f;
-    if (r + 1 < r_hi) {
-      load_state(r + 1, hn, bn);
-      load_du(r + 1, dtn, un);
-      bcn = load_bc(r + 1);
-    }
-    const float hd = 0.5f * fmul(dtc, uc);
+    const float* Bs = sBC[rr];
+    const float* Cs = sBC[rr] + NP;
+    const float hd = 0.5f * fmul(dt, uu);
     float ys[S];
 #pragma unroll
     for (int q = 0; q < S; ++q) ys[q] = 0.f;
 #pragma unroll
     for (int n = 0; n < NP; ++n) {
       const int j = n / S, q = n % S;
-      float& hs = (&hv[n / 4].x)[n % 4];
-      float& bs = (&bv[n / 4].x)[n % 4];
-      const float Bn = sBC[buf][n];
-      const float Cn = sBC[buf][NP + n];
+      float& hs = (&h4[n / 4].x)[n % 4];
+      float& bs = (&b4[n / 4].x)[n % 4];
       const float hbp = 0.5f * bs;
       float unused;
-      const float2 gw = sGate[n][tid];
-      const float g = gate_of<S, GK, false>(j, q, p.NR, has_imag, dtc, gw.x, gw.y, sTab, unused);
-      const float hb = fmul(hd, Bn);
+      const float g = gate_of<S, GK, false>(j, q, p.NR, has_imag, dt, pah[n], wh[n], sTab, unused);
+      const float hb = fmul(hd, Bs[n]);
       const float sm = hs + hbp;
       hs = ffma(g, sm, hb);
       bs = 2.f * hb;
-      ys[q] = ffma(hs, Cn, ys[q]);
+      ys[q] = ffma(hs, Cs[n], ys[q]);
     }
-    if (cvalid) {
-      p.y[(int64_t)r * p.D + c] = tree_sum<S>(ys) + fmul(uc, dsk);
-      const int64_t base = ((int64_t)r * p.D + c) * NP;
-      float4* ho4 = reinterpret_cast<float4*>(p.h_out + base);
-      float4* bo4 = reinterpret_cast<float4*>(p.beta_out + base);
-#pragma unroll
-      for (int v = 0; v < NV; ++v) {
-        ho4[v] = hv[v];
-        bo4[v] = bv[v];
-      }
-    }
-    if (tid < 2 * NP) sBC[buf ^ 1][tid] = bcn;
-    __syncthreads();  // next B / C row visible; this row no longer read
+    if (cvalid) p.y[r * p.D + c] = tree_sum<S>(ys) + fmul(uu, dsk);
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      hv[v] = hn[v];
-      bv[v] = bn[v];
+      sH[tid * NV + v] = h4[v];
+      sBt[tid * NV + v] = b4[v];
     }
-    dtc = dtn;
-    uc = un;
+    __syncthreads();  // the updated block
+    float4* ho4 = reinterpret_cast<float4*>(p.h_out) + blk;
+    float4* bo4 = reinterpret_cast<float4*>(p.beta_out) + blk;
+#pragma unroll
+    for (int m = 0; m < NV; ++m) {
+      const int k = tid + m * TCH;
+      if (FULLD || k < nvalid) {
+        store_stream(ho4 + k, sH[k]);
+        store_stream(bo4 + k, sBt[k]);
+      }
+    }
+    __syncthreads();  // the block's LDS is free for the next rollout
   }
 }
 
 template <int S, int NPL, class GK>
 static hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ctiles * p.rgroups));
-  hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK>), grid, dim3(kThreads), 0, st, p);
+  if (p.D % kStepTile == 0)
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true>), grid, dim3(kThreads), 0, st, p);
+  else
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false>), grid, dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }
 

@@ -111,6 +111,34 @@ def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
     assert torch.equal(state[1], b_scan)
 
 
+@pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8)])
+def test_step_equals_scan_many_rollouts(gpu_lib, NR, NT):
+    """Thousands of rollouts over whole 256-channel tiles (several rollouts
+    per workgroup, a short last group): still the scan's bits."""
+    from redpanda_amd.scan import hip_scan_with_state
+    hip_step = _step()
+    gen = torch.Generator().manual_seed(7 * NR + NT)
+    B, L, D = 2101, 3, 512
+    N = NR + NT
+    dt = F.softplus(torch.randn(B, L, D, generator=gen) * 0.5 - 2.0).to(dev)
+    u = torch.randn(B, L, D, generator=gen).to(dev)
+    Bc = torch.randn(B, L, N, generator=gen).to(dev)
+    Cc = torch.randn(B, L, N, generator=gen).to(dev)
+    Ar = (-torch.exp(torch.rand(D, NR, generator=gen) * 3.0)).to(dev)
+    Ai = ((torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi).to(dev)
+    Tk = torch.tanh(torch.randn(D, NT, generator=gen) * 1.5).to(dev)
+    Dz = torch.zeros(D, device=dev)
+    with torch.no_grad():
+        y_scan, (h_scan, b_scan) = hip_scan_with_state(dt, u, Bc, Cc, Ar, Ai, Tk)
+        state, ys = None, []
+        for t in range(L):
+            yt, state = hip_step(dt[:, t], u[:, t], Bc[:, t], Cc[:, t], Ar, Ai, Tk, Dz, state)
+            ys.append(yt)
+    assert torch.equal(torch.stack(ys, 1), y_scan)
+    assert torch.equal(state[0], h_scan)
+    assert torch.equal(state[1], b_scan)
+
+
 def test_scan_prefix_then_step_continues(gpu_lib):
     """scan([0, s)) state + steps over [s, L) == scan([0, L)) (bitwise)."""
     from redpanda_amd.scan import hip_scan_with_state
