@@ -57,8 +57,11 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   constexpr int CPT = (KS * CB + kThreads - 1) / kThreads;      // staged channel-steps per thread
   constexpr int SPT = (KS * NP + kThreads - 1) / kThreads;      // staged state-steps per thread
   constexpr int DPT = (K * CB + kThreads - 1) / kThreads;       // d_delta / d_u outputs per thread
+  // keep each step's h_t from the recompute (up to 40 states per channel;
+  // larger shapes recompute it in the adjoint to stay within registers)
+  constexpr bool KEEP_HT = NP <= 40;
   static_assert(K % KR == 0, "a chunk holds whole folds");
-  __shared__ float4 sCh[2][KS][CB];       // input slots: (dt, (dt*u)/2, u, dy)
+  __shared__ float4 sCh[2][KS][CB];       // input slots: (dt, (dt*u)/2, u/2, dy)
   __shared__ float sB[2][KS][NP];
   __shared__ float sC[2][KS][NP];
   __shared__ float sRed[KR][2][NRW][NP];  // per-row channel sums of dB, dC
@@ -138,7 +141,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       if (e < KS * CB) {
         const float dt = cvt_raw(rdt[k], p.dt_delta);
         const float uu = cvt_raw(ru[k], p.dt_u);
-        sCh[SL][e / CB][e % CB] = make_float4(dt, 0.5f * fmul(dt, uu), uu, rdy[k]);
+        sCh[SL][e / CB][e % CB] = make_float4(dt, 0.5f * fmul(dt, uu), 0.5f * uu, rdy[k]);
       }
     }
 #pragma unroll
@@ -280,8 +283,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 #pragma unroll
             for (int j = 0; j < NPL; ++j) hbp[j] = fmul(hdp, sB[SL][0][s * NPL + j]);
           }
-          // recompute the chunk: s_{t-1}, g_t and e*sin for every step
-          float SP[K][NPL], G[K][NPL], ES[K][NPL];
+          // recompute the chunk: s_{t-1}, g_t, e*sin and h_t for every step
+          float SP[K][NPL], G[K][NPL], ES[K][NPL], HT[KEEP_HT ? K : 1][NPL];
 #pragma unroll
           for (int m = 0; m < K; ++m) {
             if (FULL || m < kcnt) {
@@ -303,6 +306,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 G[m][j] = g;
                 ES[m][j] = es;
                 hc[j] = ffma(g, sm, hb);
+                if constexpr (KEEP_HT) HT[m][j] = hc[j];
                 hbp[j] = hb;
               }
             }
@@ -321,15 +325,18 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           for (int m = K - 1; m >= 0; --m) {
             if (FULL || m < kcnt) {
               const float4 chv = sCh[SL][m + 1][cl];
-              const float dt = chv.x, hd = chv.y, uu = chv.z, dy = chv.w;
+              const float dt = chv.x, hd = chv.y, uh = chv.z, dy = chv.w;
               float ddA = 0.f, ddB = 0.f, sBc = 0.f;
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
                 const float Bv = sB[SL][m + 1][s * NPL + j];
                 const float Cv = sC[SL][m + 1][s * NPL + j];
                 const float g = G[m][j];
-                const float hb = fmul(hd, Bv);
-                const float ht = ffma(g, SP[m][j], hb);
+                float ht;
+                if constexpr (KEEP_HT)
+                  ht = HT[m][j];
+                else
+                  ht = ffma(g, SP[m][j], fmul(hd, Bv));
                 const float q = ffma(dy, Cv, gq[j]);
                 const float dhb = q + gr[j];
                 sBc = ffma(dhb, Bv, sBc);
@@ -354,11 +361,12 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 sRed[m % KR][0][wrow][s * NPL + j] = reduce_row<S>(fmul(dhb, hd));
                 sRed[m % KR][1][wrow][s * NPL + j] = reduce_row<S>(fmul(dy, ht));
               }
-              ddA = reduce_states<S>(ddA);
-              ddB = reduce_states<S>(ddB);
+              // d(gate)/d(dt) summed over the lane's states, then over the
+              // channel's lanes with sBc; the channel's S lanes hold identical
+              // totals and store the same value
+              const float dga = reduce_states<S>(ffma(kLn2, ddA, -fmul(kRadPerStep, ddB)));
               sBc = reduce_states<S>(sBc);
-              // the channel's S lanes hold identical totals and store the same value
-              const float ddt = ffma(kLn2, ddA, -fmul(kRadPerStep, ddB)) + fmul(0.5f * uu, sBc);
+              const float ddt = dga + fmul(uh, sBc);
               const float dut = fmul(0.5f * dt, sBc);
               sDD[m][cl] = make_float2(ddt, dut);
             }
