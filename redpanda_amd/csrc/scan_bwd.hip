@@ -33,7 +33,7 @@
 // Reductions, all in a fixed order (run-to-run deterministic, no atomics):
 //   * over a channel's states (ddt, du): in-lane FMA chain + DPP butterfly;
 //   * over channels (dB, dC): DPP row rotations inside each 16-lane row, the
-//     row partials staged in LDS, then a 16-way sum per output, per tile;
+//     row partials staged in LDS, then a balanced 16-way sum per output, per tile;
 //     the per-tile partials are summed in float64 by a second kernel;
 //   * parameter gradients (dA, dTk): K-step fp32 chunk sums accumulated in
 //     float64 per lane over the batch group, then float64 across groups.
@@ -52,6 +52,10 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   constexpr int KR = NP <= 40 ? K : K / 2;  // steps per channel-sum fold
   constexpr int NFOLD = K / KR;             // folds per chunk
   constexpr int NRW = kWaves * 4;           // 16-lane rows per workgroup
+  // row partials of one output are contiguous (4 x 16-byte reads); the
+  // padding to 20 spreads the writers of a row over distinct banks
+  constexpr int RWP = NRW + 4;
+  static_assert(NRW == 16, "the fold sums 16 row partials");
   constexpr int FPT = (KR * 2 * NP + kThreads - 1) / kThreads;  // fold outputs per thread
   constexpr int KS = K + 1;  // staged steps per chunk: the step before it, then its K steps
   constexpr int CPT = (KS * CB + kThreads - 1) / kThreads;      // staged channel-steps per thread
@@ -64,7 +68,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float4 sCh[2][KS][CB];       // input slots: (dt, (dt*u)/2, u/2, dy)
   __shared__ float sB[2][KS][NP];
   __shared__ float sC[2][KS][NP];
-  __shared__ float sRed[KR][2][NRW][NP];  // per-row channel sums of dB, dC
+  __shared__ __align__(16) float sRed[KR][2][NP][RWP];  // per-row channel sums of dB, dC
   __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
   __shared__ float2 sTab[kTab];             // cos, sin of 2 pi k / kTab
   // per-thread float64 sums of the parameter gradients over the batch group
@@ -358,8 +362,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 gr[j] = gq[j];
                 // every lane of the row holds the row's total for its slice
                 // s, so the lanes sharing s store the same value
-                sRed[m % KR][0][wrow][s * NPL + j] = reduce_row<S>(fmul(dhb, hd));
-                sRed[m % KR][1][wrow][s * NPL + j] = reduce_row<S>(fmul(dy, ht));
+                sRed[m % KR][0][s * NPL + j][wrow] = reduce_row<S>(fmul(dhb, hd));
+                sRed[m % KR][1][s * NPL + j][wrow] = reduce_row<S>(fmul(dy, ht));
               }
               // d(gate)/d(dt) summed over the lane's states, then over the
               // channel's lanes with sBc; the channel's S lanes hold identical
@@ -384,9 +388,10 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   const int rem = e % (2 * p.N);
                   const int which = rem / p.N, n = rem % p.N;
                   const int kk = (n % S) * NPL + n / S;
-                  float v = sRed[e / (2 * p.N)][which][0][kk];
-#pragma unroll
-                  for (int w = 1; w < NRW; ++w) v = v + sRed[e / (2 * p.N)][which][w][kk];
+                  const float4* rp = reinterpret_cast<const float4*>(&sRed[e / (2 * p.N)][which][kk][0]);
+                  const float4 a0 = rp[0], a1 = rp[1], a2 = rp[2], a3 = rp[3];
+                  const float v = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
+                                  (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
                   *dst = dir == 0 ? v : prev[m / KR][k] + v;
                 }
               }
