@@ -2,7 +2,7 @@
 (bidirectional forward + analytic backward at the Eval-Mamba training shape)
 and the batched O(1) step (4096 rollouts x 8 layers).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step] [--no-long]
 
 One "step" of the headline workload is one forward + backward of one
 bidirectional scan layer over a batch of 256 boards x 64 tokens, d_inner 1536
@@ -14,8 +14,11 @@ forward + backward (both directions fused).
 
 Besides the headline number the JSON line carries:
   roofline      the dominant kernel's algorithmic bytes / measured duration
-                (HIP events on the launch stream) against 8 TB/s;
+                (HIP events on the launch stream) against 8 TB/s, and (the
+                scan being VALU-bound) its vector-ALU issue rate against
+                the VALU peak;
   kernels       the same for every kernel of the path;
+  long_sequence tokens/s of a causal fwd + bwd at L=2048, d_state 72;
   step          rollout-steps/s of the fused step kernel over 8 layers;
   cpu_baseline  the reference's CPU PyTorch path (the oracle's fp32
                 restatement) on a bounded sample, on this host's cores.
@@ -36,6 +39,9 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+# vector-ALU issue peak: 256 CUs x 4 SIMDs x 2.4 GHz / 4 cycles per wave64
+# fp32 instruction (16 lanes per SIMD), in wave-instructions per second
+VALU_PEAK_IPS = 256 * 4 * 2.4e9 / 4
 
 # Eval-Mamba training shape of one layer: batch 256, L=64 board tokens,
 # d_model 768, expand 2 -> d_inner 1536 (24 heads x 64), d_state 32 complex
@@ -44,6 +50,9 @@ SCAN_SHAPE = dict(B=256, L=64, D=1536, NR=32, NT=8)
 # Search-Mamba batched step: 4096 rollouts, 8 causal layers, d_model 512
 # (d_inner 1024 = 16 heads x 64), d_state 16 complex plus 4 tracking.
 STEP_SHAPE = dict(R=4096, layers=8, D=1024, NR=16, NT=4)
+# Long-sequence causal stress: batch 64, L=2048, d_inner 1024, d_state 64
+# complex plus 8 tracking, fp32 inputs.
+LONG_SHAPE = dict(B=64, L=2048, D=1024, NR=64, NT=8)
 
 
 def parse():
@@ -53,6 +62,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-step", action="store_true", help="skip the step() workload")
+    ap.add_argument("--no-long", action="store_true",
+                    help="skip the long-sequence (L=2048) scan line")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--profile-pass", action="store_true",
@@ -269,6 +280,83 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
                 t_launch=t_launch, bytes=nb, GBps=nb / t_launch / 1e9)
 
 
+def bench_long(torch, args):
+    """Causal fwd + bwd at the long-sequence shape, through the C ABI with
+    preallocated buffers (inputs generated on the device)."""
+    from redpanda_amd import _lib
+    from redpanda_amd.scan import make_scan_args
+    import torch.nn.functional as F
+    sh = LONG_SHAPE
+    B, L, D, NR, NT = sh["B"], sh["L"], sh["D"], sh["NR"], sh["NT"]
+    N = NR + NT
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1005)
+    u = torch.randn(B, L, D, generator=gen, device=dev)
+    dt = F.softplus(torch.randn(B, L, D, generator=gen, device=dev) * 0.5 - 2.0)
+    Bc = torch.randn(B, L, N, generator=gen, device=dev)
+    Cc = torch.randn(B, L, N, generator=gen, device=dev)
+    Bc = Bc / Bc.pow(2).mean(-1, keepdim=True).sqrt()
+    Cc = Cc / Cc.pow(2).mean(-1, keepdim=True).sqrt()
+    Ar = -torch.exp(torch.rand(D, NR, generator=gen, device=dev) * 3.0)
+    Ai = (torch.rand(D, NR, generator=gen, device=dev) * 2 - 1) * math.pi
+    Tk = torch.tanh(torch.randn(D, NT, generator=gen, device=dev) * 1.5)
+    dy = torch.randn(B, L, D, generator=gen, device=dev)
+    lib = _lib.load()
+    f32 = dict(dtype=torch.float32, device=dev)
+    a = make_scan_args(dt, u, Bc, Cc, Ar, Ai, Tk, False)
+    y = torch.empty((B, L, D), **f32)
+    ckpt = torch.empty(max(lib.rp_scan_ckpt_bytes(ctypes.byref(a)) // 4, 1), **f32)
+    g = [torch.empty((B, L, D), **f32), torch.empty((B, L, D), **f32),
+         torch.empty((B, L, N), **f32), torch.empty((B, L, N), **f32),
+         torch.empty((D, NR), **f32), torch.empty((D, NR), **f32), torch.empty((D, NT), **f32)]
+    work = torch.empty(max(lib.rp_scan_bwd_work_bytes(ctypes.byref(a)), 256), dtype=torch.uint8,
+                       device=dev)
+    out = _lib.ScanFwdOut(y.data_ptr(), ckpt.data_ptr(), None, None)
+    io = _lib.ScanBwdIO(dy=dy.data_ptr(), ckpt=ckpt.data_ptr(), d_delta=g[0].data_ptr(),
+                        d_u=g[1].data_ptr(), d_Bc=g[2].data_ptr(), d_Cc=g[3].data_ptr(),
+                        d_A_real=g[4].data_ptr(), d_A_imag=g[5].data_ptr(),
+                        d_track=g[6].data_ptr(), work=work.data_ptr(), work_bytes=work.numel())
+    stream = _lib.stream_of(dev)
+
+    def fwd():
+        _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out), stream), lib)
+
+    def bwd():
+        _lib.check(lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), stream), lib)
+
+    fwd()
+    bwd()
+    torch.cuda.synchronize()
+    timer = EventTimer(torch)
+    reps = max(2, min(args.steps, 5))
+    t_f = timer.time(fwd, reps)
+    t_b = timer.time(bwd, reps)
+    fb, bb = scan_bytes(B, L, D, N, NR, NT, 4, False)
+    return dict(tok_s=B * L / (t_f + t_b), t_fwd=t_f, t_bwd=t_b, fwd_bytes=fb, bwd_bytes=bb)
+
+
+def measured_valu():
+    """VALU wave-instructions per launch from the committed counter summary
+    (profiles/valu.json, written by `python -m redpanda_amd.profiling valu`
+    from an SQ_INSTS_VALU pass over `bench.py --profile-pass`), or {}."""
+    path = os.path.join(ROOT, "profiles", "valu.json")
+    try:
+        with open(path) as fh:
+            k = json.load(fh)["kernels"]
+    except (OSError, KeyError, ValueError):
+        return {}
+    return {name: v.get("SQ_INSTS_VALU") for name, v in k.items()}
+
+
+def valu_roofline(instr, seconds):
+    if not instr:
+        return None
+    ips = instr / seconds
+    return {"bound": "valu", "achieved": ips, "peak": VALU_PEAK_IPS,
+            "unit": "wave-instructions/s", "frac": ips / VALU_PEAK_IPS,
+            "instructions_per_launch": instr}
+
+
 def measured_traffic():
     """HBM bytes per launch from the committed counter summary
     (profiles/traffic.json, written by `python -m redpanda_amd.profiling
@@ -409,6 +497,12 @@ def main():
         print(f"[bench] step: {step['rollout_steps_s']:.4g} rollout-steps/s, "
               f"{step['t_launch'] * 1e6:.1f} us/launch, {step['GBps']:.0f} GB/s",
               file=sys.stderr, flush=True)
+    lng = None
+    if not args.no_long:
+        print(f"[bench] long-sequence scan {LONG_SHAPE} fp32", file=sys.stderr, flush=True)
+        lng = bench_long(torch, args)
+        print(f"[bench] long: {lng['tok_s']:.4g} tokens/s; fwd {lng['t_fwd'] * 1e3:.2f} ms, "
+              f"bwd {lng['t_bwd'] * 1e3:.2f} ms", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -420,10 +514,17 @@ def main():
     k_f, k_b = sc["kernels"][0], sc["kernels"][2]
     dom = k_b if k_b["seconds"] >= k_f["seconds"] else k_f
     tr = measured_traffic()
+    vc = measured_valu()
     roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": dom["GBps"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["GBps"] / HBM_PEAK_GBS,
             "traffic": tr.get(dom["traffic_key"]), "alg_bytes_per_launch": dom["alg_bytes"],
             "avg_launch_s": dom["seconds"]}
+    # the scan kernels are bound by the vector ALU, not by HBM: their issue
+    # rate against the VALU peak, from the committed counter pass
+    for k in sc["kernels"]:
+        key = "scan_bwd_kernel" if k["kernel"].startswith("scan_bwd") else "scan_fwd_kernel"
+        k["valu"] = valu_roofline(vc.get(key), k["seconds"]) if k["traffic_key"] else None
+    roof["valu"] = dom.get("valu")
     ms = sc["elapsed"] / args.steps * 1e3
     line = {
         "metric": "scan fwd+bwd tokens/s & %HBM peak; batched step() rollout-steps/s",
@@ -450,6 +551,14 @@ def main():
                          "traffic": tr.get("step_tile_kernel"),
                          "alg_bytes_per_launch": step["bytes"],
                          "avg_launch_s": step["t_launch"]},
+        }
+    if lng is not None:
+        line["long_sequence"] = {
+            "metric": "tokens/s", "value": lng["tok_s"],
+            "config": {"workload": "causal trapezoidal scan layer, fwd+bwd, fp32 inputs",
+                       **LONG_SHAPE, "d_state": LONG_SHAPE["NR"] + LONG_SHAPE["NT"]},
+            "fwd_s": lng["t_fwd"], "bwd_s": lng["t_bwd"],
+            "alg_bytes_fwd": lng["fwd_bytes"], "alg_bytes_bwd": lng["bwd_bytes"],
         }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

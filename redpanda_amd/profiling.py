@@ -3,6 +3,7 @@
     python -m redpanda_amd.profiling stats  <kernel_stats.csv> --cmd "<command>" > out.md
     python -m redpanda_amd.profiling traffic --fetch <pmc_fetch.csv> --write <pmc_write.csv> \
         --calib-bytes 1073741824 --out traffic.json
+    python -m redpanda_amd.profiling valu <pmc_valu.csv> --out valu.json
 
 `traffic` turns two counter passes (FETCH_SIZE, then WRITE_SIZE, each in KiB
 per dispatch) into HBM bytes per dispatch for every kernel, scaled by what
@@ -76,6 +77,22 @@ def traffic(fetch_csv, write_csv, calib_bytes):
     return out
 
 
+def valu(csv_path):
+    """Mean VALU wave-instructions (and transcendental ones) per dispatch by
+    kernel, from a pass with SQ_INSTS_VALU / SQ_INSTS_VALU_TRANS_F32."""
+    acc = collections.defaultdict(lambda: collections.defaultdict(list))
+    with open(csv_path) as fh:
+        for row in csv.DictReader(fh):
+            if CALIB_MARK in row["Kernel_Name"]:
+                continue
+            acc[short_name(row["Kernel_Name"])][row["Counter_Name"]].append(float(row["Counter_Value"]))
+    out = {}
+    for k, ctrs in acc.items():
+        out[k] = {name: sum(v) / len(v) for name, v in ctrs.items()}
+    return {"counters": "mean per dispatch; wave-instructions summed over the device",
+            "kernels": out}
+
+
 def stats_markdown(csv_path, cmd, title):
     rows = list(csv.DictReader(open(csv_path)))
     lines = [f"# {title}", "", "Command (repo root, one MI355X):", "", f"    {cmd}", "",
@@ -103,9 +120,19 @@ def main(argv=None):
     t.add_argument("--write", required=True)
     t.add_argument("--calib-bytes", type=int, default=1 << 30)
     t.add_argument("--out")
+    v = sub.add_parser("valu")
+    v.add_argument("csv")
+    v.add_argument("--out")
     a = ap.parse_args(argv)
     if a.action == "stats":
         sys.stdout.write(stats_markdown(a.csv, a.cmd, a.title))
+    elif a.action == "valu":
+        text = json.dumps(valu(a.csv), indent=1, sort_keys=True)
+        if a.out:
+            with open(a.out, "w") as fh:
+                fh.write(text + "\n")
+        else:
+            print(text)
     else:
         res = traffic(a.fetch, a.write, a.calib_bytes)
         text = json.dumps(res, indent=1, sort_keys=True)
