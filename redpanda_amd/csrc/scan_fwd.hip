@@ -3,11 +3,12 @@
 // Replaces the reference's _fwd_kernel (engine/triton_scan.py:44-98) and its
 // two-launch bidirectional wrapper (engine/mamba.py:254-260).  One workgroup
 // = 4 waves = CB channels of one batch row; each lane carries NPL states of
-// one channel in VGPRs and walks the sequence serially.  Per block of
-// kFwdTB steps the workgroup stages dt, (dt*u)/2, B and C into LDS (converted
-// to fp32 once), then every wave runs the recurrence out of LDS.  In
-// bidirectional mode the same workgroup runs the reversed direction next and
-// accumulates into y, so inputs are read from HBM once per direction and
+// one channel in VGPRs and walks the sequence serially.  Per block of 32
+// steps (16 above 40 states) the workgroup stages dt, (dt*u)/2, B and C into
+// LDS (converted to fp32 once), then every wave runs the recurrence out of
+// LDS and leaves the block's y in LDS, written out coalesced once per block.
+// In bidirectional mode the same workgroup runs the reversed direction next
+// and accumulates into y, so inputs are read from HBM once per direction and
 // there are no flip copies.
 //
 // Optional outputs: per-chunk state checkpoints for the backward, and the
@@ -21,10 +22,13 @@ namespace rp {
 template <int S, int NPL, class GK>
 __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut o) {
   using Sh = Shape<S, NPL>;
-  constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = kFwdTB;
+  // steps staged per block: fewer for large states, whose B / C rows
+  // dominate the LDS (occupancy)
+  constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = NP > 40 ? kFwdTB / 2 : kFwdTB;
   __shared__ float2 sDH[TB][CB];   // (dt, (dt*u)/2) per step and channel
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
+  __shared__ float sY[TB][CB];     // the block's y, written out channel-contiguous
   __shared__ float2 sTab[kTab];      // cos, sin of 2 pi k / kTab
 
   const int tid = threadIdx.x;
@@ -55,10 +59,25 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
         hbp[j] = 0.5f * p.beta0[idx];
       }
     }
+    // y of the block starting at step i0 (cnt steps) from sY: coalesced, and
+    // the reverse direction adds to what the forward direction stored
+    auto write_y = [&](int i0, int cnt) {
+      for (int e = tid; e < cnt * CB; e += kThreads) {
+        const int r = e / CB, ci = e % CB;
+        const int c2 = tile * CB + ci;
+        if (c2 < p.D) {
+          const int i = i0 + r;
+          const int t = dir ? (L - 1 - i) : i;
+          float* yp = o.y + ((int64_t)b * L + t) * p.D + c2;
+          *yp = dir == 0 ? sY[r][ci] : *yp + sY[r][ci];
+        }
+      }
+    };
     for (int bi = 0; bi < nblk; ++bi) {
       const int i0 = bi * TB;
       const int cnt = min(TB, L - i0);
       __syncthreads();
+      if (bi > 0) write_y(i0 - TB, TB);
       for (int e = tid; e < TB * CB; e += kThreads) {
         const int r = e / CB, ci = e % CB;
         const int c2 = tile * CB + ci;
@@ -98,16 +117,13 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
         const float2 dh = sDH[r][cl];
         float y = fwd_update<S, NPL, GK>(h, hbp, gp, sTab, dh.x, dh.y, &sB[r][s * NPL],
                                          &sC[r][s * NPL], s, p.NR, has_imag);
-        y = reduce_states<S>(y);
-        if (s == 0 && cvalid) {
-          const int t = dir ? (L - 1 - i) : i;
-          float* yp = o.y + ((int64_t)b * L + t) * p.D + c;
-          if (dir == 0)
-            *yp = y;
-          else
-            *yp = *yp + y;
-        }
+        // the channel's S lanes hold the same total and store the same value
+        sY[r][cl] = reduce_states<S>(y);
       }
+    }
+    if (nblk > 0) {
+      __syncthreads();
+      write_y((nblk - 1) * TB, L - (nblk - 1) * TB);
     }
     if (dir == 0 && o.h_last != nullptr && cvalid) {
 #pragma unroll
