@@ -471,6 +471,47 @@ def cpu_baseline(budget_s):
             "torch": torch.__version__}
 
 
+def cpu_step_baseline(budget_s):
+    """The reference's per-layer torch step (engine/mamba.py:466-494; the
+    oracle's fp32 restatement) at the step workload's layer shape over all
+    8 layers, on a bounded sample of rollouts, on this host's cores."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import scan_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    sh = STEP_SHAPE
+    R, D, NR, NT = 256, sh["D"], sh["NR"], sh["NT"]
+    N = NR + NT
+    gen = torch.Generator().manual_seed(1004)
+    layers = []
+    for _ in range(sh["layers"]):  # parameters and one ply's inputs per layer
+        layers.append(dict(
+            Ar=-torch.exp(torch.rand(D, NR, generator=gen) * 3.0),
+            Ai=(torch.rand(D, NR, generator=gen) * 2 - 1) * math.pi,
+            Tk=torch.tanh(torch.randn(D, NT, generator=gen) * 1.5),
+            Dk=torch.randn(D, generator=gen),
+            dt=F.softplus(torch.randn(R, D, generator=gen) * 0.5 - 2.0),
+            u=torch.randn(R, D, generator=gen),
+            Bc=torch.randn(R, N, generator=gen), Cc=torch.randn(R, N, generator=gen)))
+    state = [None] * sh["layers"]
+
+    def ply():
+        for i, lp in enumerate(layers):
+            _, state[i] = scan_ref.step_core_ref(lp["dt"], lp["u"], lp["Bc"], lp["Cc"], lp["Ar"],
+                                                 lp["Ai"], lp["Tk"], lp["Dk"], state[i])
+
+    ply()
+    plies, t0 = 0, time.perf_counter()
+    while plies < 3 or (time.perf_counter() - t0 < budget_s and plies < 50):
+        ply()
+        plies += 1
+    el = time.perf_counter() - t0
+    return {"value": R * plies / el, "unit": "rollout-steps/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"oracle fp32 restatement of the reference torch step (SSM core), "
+                       f"{sh['layers']} layers, R={R} rollouts, D={D} N={N}, {plies} plies")}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -509,6 +550,10 @@ def main():
         cpu = cpu_baseline(args.cpu_seconds)
         print(f"[bench] cpu: {cpu['value']:.4g} tokens/s on {cpu['cores']} threads",
               file=sys.stderr, flush=True)
+        if step is not None:
+            step["cpu_baseline"] = cpu_step_baseline(args.cpu_seconds / 3)
+            print(f"[bench] cpu step: {step['cpu_baseline']['value']:.4g} rollout-steps/s",
+                  file=sys.stderr, flush=True)
 
     # dominant kernel: the longer of forward (training) and backward
     k_f, k_b = sc["kernels"][0], sc["kernels"][2]
@@ -551,6 +596,7 @@ def main():
                          "traffic": tr.get("step_tile_kernel"),
                          "alg_bytes_per_launch": step["bytes"],
                          "avg_launch_s": step["t_launch"]},
+            "cpu_baseline": step.get("cpu_baseline"),
         }
     if lng is not None:
         line["long_sequence"] = {
