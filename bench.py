@@ -276,8 +276,18 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
     timer = EventTimer(torch)
     t_launch = timer.time(ply, plies) / layers
     nb = step_bytes(R, D, N, NR, NT)
+    # the first ply after a batch-1 cache is fanned out to the R rollouts:
+    # every rollout reads the one shared state (no expand copies)
+    a0, keep0 = per_layer[0]
+    shared_h = torch.randn((1, D, N), generator=gen).to(dev)
+    shared_b = torch.randn((1, D, N), generator=gen).to(dev)
+    ab = _lib.StepArgs.from_buffer_copy(a0)
+    ab.h_in, ab.beta_in, ab.broadcast_state = shared_h.data_ptr(), shared_b.data_ptr(), 1
+    t_shared = timer.time(lambda: _lib.check(lib.rp_step(ctypes.byref(ab), stream), lib), 10)
+    nb_shared = R * (8 * D * N + 12 * D + 8 * N) + 8 * D * N + (2 * D * NR + D * NT + D) * 4
     return dict(rollout_steps_s=R * plies / elapsed, plies=plies, elapsed=elapsed,
-                t_launch=t_launch, bytes=nb, GBps=nb / t_launch / 1e9)
+                t_launch=t_launch, bytes=nb, GBps=nb / t_launch / 1e9,
+                t_shared=t_shared, bytes_shared=nb_shared, GBps_shared=nb_shared / t_shared / 1e9)
 
 
 def bench_long(torch, args):
@@ -597,6 +607,11 @@ def main():
                          "alg_bytes_per_launch": step["bytes"],
                          "avg_launch_s": step["t_launch"]},
             "cpu_baseline": step.get("cpu_baseline"),
+            "from_shared_state": {
+                "workload": "first ply after a batch-1 cache is fanned out to the rollouts "
+                            "(broadcast input state, no copies)",
+                "avg_launch_s": step["t_shared"], "alg_bytes_per_launch": step["bytes_shared"],
+                "achieved_GBps": step["GBps_shared"]},
         }
     if lng is not None:
         line["long_sequence"] = {

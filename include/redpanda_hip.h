@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 1
+#define RP_ABI_VERSION 2
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -125,6 +125,10 @@ typedef struct rp_scan_bwd_io {
  * contiguous (may alias h_in / beta_in for an in-place update); y: (R, D)
  * fp32 contiguous = sum_n h_out C + u D.  beta_out = (dt u) B exactly as the
  * reference stores dBu_t.
+ * broadcast_state = 1: h_in and beta_in hold ONE (D, N) state that every
+ * rollout continues from -- a batch-1 cache fanned out to R rollouts without
+ * the copies of engine/search_mamba.py:177-187 (expand().contiguous()); the
+ * outputs must then not overlap the inputs.  0: the (R, D, N) layout above.
  */
 typedef struct rp_step_args {
   int64_t R, D, N, NR, NT;
@@ -141,6 +145,8 @@ typedef struct rp_step_args {
   float* h_out;
   float* beta_out;
   float* y;
+  int32_t broadcast_state;  /* 0 or 1, see above */
+  int32_t reserved;         /* must be 0 */
 } rp_step_args;
 
 /* ABI version this library was built with (RP_ABI_VERSION). */

@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -56,6 +56,7 @@ class StepArgs(ctypes.Structure):
         ("Bc", _vp), ("Bc_sr", _i64), ("Cc", _vp), ("Cc_sr", _i64),
         ("h_in", _vp), ("beta_in", _vp), ("A_real", _vp), ("A_imag", _vp), ("track", _vp),
         ("Dskip", _vp), ("h_out", _vp), ("beta_out", _vp), ("y", _vp),
+        ("broadcast_state", _i32), ("reserved", _i32),
     ]
 
 

@@ -31,6 +31,12 @@ constexpr int64_t kI32Max = 0x7fffffff;
 
 bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Whether byte ranges [a, a + na) and [b, b + nb) intersect.
+bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + (uintptr_t)nb && y < x + (uintptr_t)na;
+}
+
 int64_t elem_size(int dtype) { return dtype == RP_F32 ? 4 : 2; }
 
 int64_t round_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
@@ -344,6 +350,20 @@ int rp_step_check(const rp_step_args* a) {
     return fail(RP_ERR_INVALID, "step args: NULL required pointer");
   if ((a->h_in == nullptr) != (a->beta_in == nullptr))
     return fail(RP_ERR_INVALID, "step args: h_in and beta_in go together");
+  if ((a->broadcast_state != 0 && a->broadcast_state != 1) || a->reserved != 0)
+    return fail(RP_ERR_INVALID, "step args: broadcast_state must be 0 or 1, reserved 0");
+  if (a->broadcast_state && a->h_in == nullptr)
+    return fail(RP_ERR_INVALID, "step args: broadcast_state needs h_in / beta_in");
+  if (a->broadcast_state) {
+    // every rollout reads the one input state while others write theirs
+    const int64_t in_bytes = a->D * a->N * 4, out_bytes = a->R * a->D * a->N * 4;
+    const float* ins[] = {a->h_in, a->beta_in};
+    const float* outs[] = {a->h_out, a->beta_out};
+    for (const float* i : ins)
+      for (const float* o : outs)
+        if (overlaps(i, in_bytes, o, out_bytes))
+          return fail(RP_ERR_INVALID, "step args: a broadcast input state overlaps an output");
+  }
   if (a->NR > 0 && !a->A_real) return fail(RP_ERR_INVALID, "step args: NR>0 needs A_real");
   if (a->NR == 0 && a->A_imag) return fail(RP_ERR_INVALID, "step args: A_imag without NR");
   if (a->NT > 0 && !a->track) return fail(RP_ERR_INVALID, "step args: NT>0 needs track");
@@ -379,6 +399,7 @@ int rp_step(const rp_step_args* a, void* stream) {
   p.csr = a->Cc_sr;
   p.h_in = a->h_in;
   p.beta_in = a->beta_in;
+  p.ssr = a->broadcast_state ? 0 : a->D * a->N;
   p.Ar = a->NR > 0 ? a->A_real : nullptr;
   p.Ai = a->NR > 0 ? a->A_imag : nullptr;
   p.Tk = a->NT > 0 ? a->track : nullptr;

@@ -67,6 +67,7 @@ struct StepParams {
   int64_t csr;
   const float* h_in;
   const float* beta_in;
+  int64_t ssr;  // elements between consecutive rollouts' input states (0: one shared state)
   const float* Ar;
   const float* Ai;
   const float* Tk;

@@ -53,7 +53,8 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
     dt = p.delta[(int64_t)r * p.dsr + c];
     uu = p.u[(int64_t)r * p.usr + c];
   }
-  const int64_t sbase = ((int64_t)r * p.D + c) * p.N;
+  const int64_t sbase = ((int64_t)r * p.D + c) * p.N;  // output state
+  const int64_t ibase = (int64_t)r * p.ssr + (int64_t)c * p.N;  // input state
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     const int n = j * S + s;
@@ -66,8 +67,8 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
       Cs[j] = p.Cc[(int64_t)r * p.csr + n];
     }
     if (cvalid && n < p.N && p.h_in != nullptr) {
-      h[j] = p.h_in[sbase + n];
-      hbp[j] = 0.5f * p.beta_in[sbase + n];
+      h[j] = p.h_in[ibase + n];
+      hbp[j] = 0.5f * p.beta_in[ibase + n];
     }
   }
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
@@ -196,15 +197,17 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   // (thread t moves float4s t, t+256, ...) into LDS; each thread updates its
   // channel's states there; coalesced streaming stores write the block back.
   // Every input is in LDS or registers before the first store, so h_out and
-  // beta_out may alias h_in and beta_in.
+  // beta_out may alias h_in and beta_in (per-rollout states).
   for (int rr = 0; rr < nr; ++rr) {
     const int64_t r = r_lo + rr;
-    const int64_t blk = (r * p.D + c0) * NV;  // float4 offset of the block
+    const int64_t blk = (r * p.D + c0) * NV;  // float4 offset of the output block
     const float dt = p.delta[r * p.dsr + cld];
     const float uu = p.u[r * p.usr + cld];
     if (p.h_in != nullptr) {
-      const float4* hi4 = reinterpret_cast<const float4*>(p.h_in) + blk;
-      const float4* bi4 = reinterpret_cast<const float4*>(p.beta_in) + blk;
+      // input block: the rollout's own, or the one shared state (ssr == 0)
+      const int64_t iblk = r * (p.ssr / 4) + (int64_t)c0 * NV;
+      const float4* hi4 = reinterpret_cast<const float4*>(p.h_in) + iblk;
+      const float4* bi4 = reinterpret_cast<const float4*>(p.beta_in) + iblk;
       float4 hl[NV], bl[NV];
 #pragma unroll
       for (int m = 0; m < NV; ++m) {

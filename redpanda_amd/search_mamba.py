@@ -103,10 +103,15 @@ class SearchMamba(nn.Module):
 
     @staticmethod
     def _expand_cache(cache, k):
-        """Broadcast a batch-1 cache to k rows as contiguous copies
-        (engine/search_mamba.py:177-187)."""
-        return [(h.expand(k, *h.shape[1:]).contiguous(), b.expand(k, *b.shape[1:]).contiguous())
-                for h, b in cache]
+        """Broadcast a batch-1 cache to k rows (engine/search_mamba.py:177-187).
+
+        The reference materialises k copies (expand().contiguous()); here the
+        rows are stride-0 views of the one state, which the step kernel reads
+        in place, and every step returns fresh per-row states.  Callers that
+        clone or concatenate the cache get contiguous tensors as before; an
+        in-place write into the returned views is not supported (torch
+        rejects it)."""
+        return [(h.expand(k, *h.shape[1:]), b.expand(k, *b.shape[1:])) for h, b in cache]
 
     @torch.no_grad()
     def evaluate_lines_fast(self, board_encoding, move_sequences, lengths=None):

@@ -6,6 +6,10 @@ the (h, beta) state once and writes the new state once.  The new state is a
 pair of fresh tensors, as in the reference (callers clone / cat / expand cached
 states, engine/mars_search.py:222-224, engine/search_mamba.py:177-187), unless
 `out` passes preallocated (possibly aliasing) buffers.
+
+A state that is an expanded view of one (D, N) state -- a batch-1 cache
+fanned out to R rollouts, as SearchMamba._expand_cache returns it -- is read
+in place by every rollout (no copies).
 """
 
 import ctypes
@@ -24,13 +28,26 @@ def _rows(t):
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _state_pair(h, b, R, D, N):
+    """(h, beta, broadcast) for the kernel: per-rollout contiguous states, or
+    one shared (D, N) state when both are stride-0 expansions of one."""
+    if h.shape != (R, D, N) or b.shape != (R, D, N):
+        raise ValueError(f"step: state must be (R, D, N) = {(R, D, N)}")
+    h = h.to(torch.float32)
+    b = b.to(torch.float32)
+    if R > 1 and h.stride(0) == 0 and b.stride(0) == 0 and h[0].is_contiguous() and \
+            b[0].is_contiguous():
+        return h, b, 1
+    return h.contiguous(), b.contiguous(), 0
+
+
 def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None):
     """One step for R rollouts.
 
     delta, u: (R, D); Bc, Cc: (R, N) (contracted over p); A_real/A_imag:
     (D, NR) or None; track: (D, NT) or None; Dskip: (D,); state: (h, beta)
-    fp32 (R, D, N) or None for a fresh state.  Returns (y (R, D) incl. u*D,
-    (h_new, beta_new)).
+    fp32 (R, D, N) (or an expansion of one (1, D, N) state) or None for a
+    fresh state.  Returns (y (R, D) incl. u*D, (h_new, beta_new)).
     """
     lib = _lib.load()
     R, D = u.shape
@@ -48,12 +65,9 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     Tk = None if track is None else _f32c(track.detach())
     Dk = _f32c(Dskip.detach())
     h_in = beta_in = None
+    broadcast = 0
     if state is not None:
-        h_in, beta_in = state
-        if h_in.shape != (R, D, N) or beta_in.shape != (R, D, N):
-            raise ValueError(f"step: state must be (R, D, N) = {(R, D, N)}")
-        h_in = _f32c(h_in)
-        beta_in = _f32c(beta_in)
+        h_in, beta_in, broadcast = _state_pair(state[0], state[1], R, D, N)
     if out is None:
         h_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
         beta_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
@@ -70,5 +84,6 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     a.A_real, a.A_imag, a.track = _lib.ptr(Ar), _lib.ptr(Ai), _lib.ptr(Tk)
     a.Dskip = Dk.data_ptr()
     a.h_out, a.beta_out, a.y = h_out.data_ptr(), beta_out.data_ptr(), y.data_ptr()
+    a.broadcast_state = broadcast
     _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
     return y, (h_out, beta_out)

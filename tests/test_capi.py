@@ -133,6 +133,22 @@ def test_step_check(lib):
     assert lib.rp_step_check(ctypes.byref(_step_args(NT=5))) < 0
 
 
+def test_step_broadcast_state_rules(lib):
+    # one shared (D, N) input state read by every rollout, outputs elsewhere
+    ok = dict(broadcast_state=1, h_in=0x100000, beta_in=0x200000, h_out=0x300000,
+              beta_out=0x400000)
+    assert lib.rp_step_check(ctypes.byref(_step_args(**ok))) == 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "broadcast_state": 2}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "reserved": 1}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "h_in": None,
+                                                         "beta_in": None}))) < 0
+    # in place would let one rollout overwrite the state the others still read
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "h_out": 0x100000}))) < 0
+    assert "overlaps" in lib.rp_last_error().decode()
+    # the output block (R*D*N*4 bytes) reaching into the shared input
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "beta_out": 0x200000 - 64}))) < 0
+
+
 def test_initial_state_rules(lib):
     f = 0x10000
     assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f))) == 0

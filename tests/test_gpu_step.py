@@ -194,6 +194,23 @@ def test_batched_equals_singles_and_chains(gpu_lib):
             assert torch.equal(si[0][0], chain[0][i])
 
 
+@pytest.mark.parametrize("R,D,NR,NT", [(300, 512, 16, 4), (37, 100, 12, 8), (64, 256, 20, 5)])
+def test_broadcast_state_equals_copies(gpu_lib, R, D, NR, NT):
+    """A (1, D, N) state expanded to R rollouts (a stride-0 view, read in
+    place) steps exactly like its materialised copies."""
+    hip_step = _step()
+    c = make_step_case(5 * R + NT, R=R, D=D, NR=NR, NT=NT)
+    p = [to(c[k]) for k in ("delta", "u", "Bc", "Cc", "Ar", "Ai", "Tk", "D")]
+    h1, b1 = to(c["h"][:1]), to(c["beta"][:1])
+    hv, bv = h1.expand(R, -1, -1), b1.expand(R, -1, -1)
+    assert hv.stride(0) == 0
+    with torch.no_grad():
+        y_v, (h_v, b_v) = hip_step(*p, (hv, bv))
+        y_c, (h_c, b_c) = hip_step(*p, (hv.contiguous(), bv.contiguous()))
+    assert torch.equal(y_v, y_c) and torch.equal(h_v, h_c) and torch.equal(b_v, b_c)
+    assert torch.equal(h1, to(c["h"][:1]))  # the shared input is untouched
+
+
 def test_in_place_state_update(gpu_lib):
     hip_step = _step()
     c = make_step_case(43, R=4, D=64, NR=16, NT=4)
