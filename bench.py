@@ -20,6 +20,8 @@ Besides the headline number the JSON line carries:
   kernels       the same for every kernel of the path;
   long_sequence tokens/s of a causal fwd + bwd at L=2048, d_state 72;
   step          rollout-steps/s of the fused step kernel over 8 layers;
+  mixer_gate    the fused (y + 2 u D) silu(z) gate after the scan: kernel
+                durations and bytes, and fwd + bwd against torch's ops;
   cpu_baseline  the reference's CPU PyTorch path (the oracle's fp32
                 restatement) on a bounded sample, on this host's cores.
 Only one GPU is used; --gpus above 1 exits with a message.
@@ -290,6 +292,83 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
                 t_shared=t_shared, bytes_shared=nb_shared, GBps_shared=nb_shared / t_shared / 1e9)
 
 
+def mixer_inputs(torch, dev, seed):
+    """The mixer gate's operands at the scan shape: y fp32 from the scan,
+    u bf16, z bf16 as the second half of a (B, L, 2 d_inner) in_proj output."""
+    B, L, D = SCAN_SHAPE["B"], SCAN_SHAPE["L"], SCAN_SHAPE["D"]
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    y = torch.randn(B, L, D, generator=gen, device=dev)
+    u = torch.randn(B, L, D, generator=gen, device=dev).to(torch.bfloat16)
+    z = (torch.randn(B, L, 2 * D, generator=gen, device=dev) * 2).to(torch.bfloat16)
+    z = z.chunk(2, dim=-1)[1]
+    Dp = torch.randn(D, generator=gen, device=dev)
+    dout = torch.randn(B, L, D, generator=gen, device=dev)
+    return y, u, z, Dp, dout
+
+
+def mixer_bytes(n):
+    """Algorithmic HBM bytes of the gate over n = B*L*d_inner elements
+    (bf16 u and z, fp32 y, out, dout, dy): forward reads y, u, z and writes
+    out; backward reads y, u, z, dout and writes dy, du, dz."""
+    return n * (4 + 2 + 2 + 4), n * (4 + 2 + 2 + 4 + 4 + 2 + 2)
+
+
+def bench_mixer(torch, args):
+    """The fused output gate (y + 2 u D) silu(z) of a bidirectional layer:
+    kernel durations through the C ABI, and fwd + bwd through autograd
+    against the same ops run by torch (what the reference executes)."""
+    import torch.nn.functional as F
+    from redpanda_amd import _lib
+    from redpanda_amd.mixer import hip_mixer_out, make_mixer_args
+    dev = torch.device("cuda:0")
+    y, u, z, Dp, dout = mixer_inputs(torch, dev, 1007)
+    lib = _lib.load()
+    out = torch.empty_like(y)
+    a = make_mixer_args(y, u, z, Dp, 2, out)
+    dy = torch.empty_like(y)
+    du = torch.empty_like(u)
+    dz = torch.empty(u.shape, dtype=z.dtype, device=dev)
+    dD = torch.empty_like(Dp)
+    work = torch.empty(max(lib.rp_mixer_out_work_bytes(ctypes.byref(a)), 256),
+                       dtype=torch.uint8, device=dev)
+    g = _lib.MixerOutGrad(dout=dout.data_ptr(), dy=dy.data_ptr(), du=du.data_ptr(),
+                          dz=dz.data_ptr(), dD=dD.data_ptr(), work=work.data_ptr(),
+                          work_bytes=work.numel())
+    stream = _lib.stream_of(dev)
+
+    def fwd():
+        _lib.check(lib.rp_mixer_out_fwd(ctypes.byref(a), stream), lib)
+
+    def bwd():
+        _lib.check(lib.rp_mixer_out_bwd(ctypes.byref(a), ctypes.byref(g), stream), lib)
+
+    leaves = [t.detach().clone().requires_grad_() for t in (y, u, z, Dp)]
+
+    def fused_autograd():
+        for t in leaves:
+            t.grad = None
+        hip_mixer_out(*leaves, 2).backward(dout)
+
+    def torch_autograd():
+        for t in leaves:
+            t.grad = None
+        yv, uv, zv, Dv = leaves
+        ((yv + uv * Dv + uv * Dv) * F.silu(zv)).backward(dout)
+
+    for fn in (fwd, bwd, fused_autograd, torch_autograd):
+        fn()
+    torch.cuda.synchronize()
+    timer = EventTimer(torch)
+    reps = max(args.steps, 10)
+    t_f = timer.time(fwd, reps)
+    t_b = timer.time(bwd, reps)
+    t_fused = timer.time(fused_autograd, reps)
+    t_torch = timer.time(torch_autograd, reps)
+    fb, bb = mixer_bytes(y.numel())
+    return dict(t_fwd=t_f, t_bwd=t_b, fwd_bytes=fb, bwd_bytes=bb, t_fused=t_fused,
+                t_torch=t_torch)
+
+
 def bench_long(torch, args):
     """Causal fwd + bwd at the long-sequence shape, through the C ABI with
     preallocated buffers (inputs generated on the device)."""
@@ -418,6 +497,23 @@ def profile_pass(torch):
     del y, ckpt, g, work, c
     args = argparse.Namespace(warmup=3)
     step_layers = bench_step(torch, args, layers=1, plies=3, keep=False)
+    # the mixer gate, three dispatches each way
+    from redpanda_amd.mixer import make_mixer_args
+    my, mu, mz, mD, mdout = mixer_inputs(torch, dev, 1007)
+    mout = torch.empty_like(my)
+    ma = make_mixer_args(my, mu, mz, mD, 2, mout)
+    mg_t = [torch.empty_like(my), torch.empty_like(mu), torch.empty_like(mu),
+            torch.empty_like(mD),
+            torch.empty(max(lib.rp_mixer_out_work_bytes(ctypes.byref(ma)), 256),
+                        dtype=torch.uint8, device=dev)]
+    mg = _lib.MixerOutGrad(dout=mdout.data_ptr(), dy=mg_t[0].data_ptr(), du=mg_t[1].data_ptr(),
+                           dz=mg_t[2].data_ptr(), dD=mg_t[3].data_ptr(),
+                           work=mg_t[4].data_ptr(), work_bytes=mg_t[4].numel())
+    for _ in range(3):
+        _lib.check(lib.rp_mixer_out_fwd(ctypes.byref(ma), stream), lib)
+        _lib.check(lib.rp_mixer_out_bwd(ctypes.byref(ma), ctypes.byref(mg), stream), lib)
+    torch.cuda.synchronize()
+    del my, mu, mz, mD, mdout, mout, mg_t
     # calibration: one elementwise dispatch that reads 1 GiB and writes 1 GiB
     # (a device-to-device copy_ is split into several copy dispatches)
     src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
@@ -554,6 +650,12 @@ def main():
         lng = bench_long(torch, args)
         print(f"[bench] long: {lng['tok_s']:.4g} tokens/s; fwd {lng['t_fwd'] * 1e3:.2f} ms, "
               f"bwd {lng['t_bwd'] * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    mix = bench_mixer(torch, args)
+    print(f"[bench] mixer gate: fwd {mix['t_fwd'] * 1e6:.1f} us "
+          f"({mix['fwd_bytes'] / mix['t_fwd'] / 1e9:.0f} GB/s), bwd {mix['t_bwd'] * 1e6:.1f} us "
+          f"({mix['bwd_bytes'] / mix['t_bwd'] / 1e9:.0f} GB/s); fwd+bwd autograd "
+          f"{mix['t_fused'] * 1e6:.1f} us fused vs {mix['t_torch'] * 1e6:.1f} us torch ops",
+          file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -621,6 +723,21 @@ def main():
             "fwd_s": lng["t_fwd"], "bwd_s": lng["t_bwd"],
             "alg_bytes_fwd": lng["fwd_bytes"], "alg_bytes_bwd": lng["bwd_bytes"],
         }
+    line["mixer_gate"] = {
+        "workload": "(y + 2 u D) silu(z) of the bidirectional layer at the scan shape, "
+                    "bf16 u / z (z a chunk of the in_proj output), fp32 y and gradients",
+        "fwd": {"kernel": "mixer_out_fwd_kernel", "avg_launch_s": mix["t_fwd"],
+                "alg_bytes_per_launch": mix["fwd_bytes"],
+                "achieved_GBps": mix["fwd_bytes"] / mix["t_fwd"] / 1e9,
+                "frac": mix["fwd_bytes"] / mix["t_fwd"] / 1e9 / HBM_PEAK_GBS,
+                "traffic": tr.get("mixer_out_fwd_kernel")},
+        "bwd": {"kernel": "mixer_out_bwd_kernel + reduction", "avg_launch_s": mix["t_bwd"],
+                "alg_bytes_per_launch": mix["bwd_bytes"],
+                "achieved_GBps": mix["bwd_bytes"] / mix["t_bwd"] / 1e9,
+                "frac": mix["bwd_bytes"] / mix["t_bwd"] / 1e9 / HBM_PEAK_GBS,
+                "traffic": tr.get("mixer_out_bwd_kernel")},
+        "fwd_bwd_autograd_s": {"fused": mix["t_fused"], "torch_ops": mix["t_torch"]},
+    }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 

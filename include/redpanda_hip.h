@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 2
+#define RP_ABI_VERSION 3
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -148,6 +148,57 @@ typedef struct rp_step_args {
   int32_t broadcast_state;  /* 0 or 1, see above */
   int32_t reserved;         /* must be 0 */
 } rp_step_args;
+
+/*
+ * The mixer's output gate around the scan (engine/mamba.py:262-265, with the
+ * D-skip of :350 / :375): out = (y + k u D) * silu(z), k = 1 for a causal
+ * layer, 2 for a bidirectional one (the skip is added once per direction).
+ * y: (B, L, D) fp32 contiguous (the scan output); u, z: (B, L, D) with batch
+ * and time strides, inner stride 1, each RP_F32 / RP_BF16 / RP_F16; Dskip:
+ * (D,) fp32; out: (B, L, D) fp32 contiguous (may be y itself; unused, and
+ * may be NULL, for the backward).  silu(z) is rounded to z's
+ * dtype before the product, as torch's ops on those dtypes do.
+ */
+typedef struct rp_mixer_out_args {
+  int64_t B, L, D;
+  int32_t k_skip;          /* 1 or 2 */
+  int32_t dtype_u, dtype_z;
+  int32_t reserved;        /* must be 0 */
+  const float* y;
+  const void* u;  int64_t u_sb, u_sl;
+  const void* z;  int64_t z_sb, z_sl;
+  const float* Dskip;
+  float* out;
+} rp_mixer_out_args;
+
+/*
+ * Its backward given dout (B, L, D) fp32 contiguous: dy (fp32, the scan's
+ * upstream gradient), du (u's dtype, the skip's share only), dz (z's dtype),
+ * all (B, L, D) contiguous; dD (D,) fp32 (deterministic sums).  work:
+ * rp_mixer_out_work_bytes() of scratch.
+ */
+typedef struct rp_mixer_out_grad {
+  const float* dout;
+  float* dy;
+  void* du;
+  void* dz;
+  float* dD;
+  void* work;
+  int64_t work_bytes;
+} rp_mixer_out_grad;
+
+/* Validate mixer-output arguments on the host without launching anything. */
+int rp_mixer_out_check(const rp_mixer_out_args* a);
+
+/* Bytes of scratch rp_mixer_out_bwd needs. */
+int64_t rp_mixer_out_work_bytes(const rp_mixer_out_args* a);
+
+/* out = (y + k u D) * silu(z); replaces the elementwise ops after the scan
+ * in Mamba3Block.forward (engine/mamba.py:262-265, :350). */
+int rp_mixer_out_fwd(const rp_mixer_out_args* a, void* stream);
+
+/* The autograd of those ops in one pass (plus a small dD reduction). */
+int rp_mixer_out_bwd(const rp_mixer_out_args* a, const rp_mixer_out_grad* g, void* stream);
 
 /* ABI version this library was built with (RP_ABI_VERSION). */
 int rp_abi_version(void);

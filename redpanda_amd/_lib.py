@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -60,6 +60,22 @@ class StepArgs(ctypes.Structure):
     ]
 
 
+class MixerOutArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", _i64), ("L", _i64), ("D", _i64),
+        ("k_skip", _i32), ("dtype_u", _i32), ("dtype_z", _i32), ("reserved", _i32),
+        ("y", _vp), ("u", _vp), ("u_sb", _i64), ("u_sl", _i64),
+        ("z", _vp), ("z_sb", _i64), ("z_sl", _i64), ("Dskip", _vp), ("out", _vp),
+    ]
+
+
+class MixerOutGrad(ctypes.Structure):
+    _fields_ = [
+        ("dout", _vp), ("dy", _vp), ("du", _vp), ("dz", _vp), ("dD", _vp),
+        ("work", _vp), ("work_bytes", _i64),
+    ]
+
+
 # Every symbol include/redpanda_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "rp_abi_version": (ctypes.c_int, []),
@@ -71,6 +87,11 @@ SIGNATURES = {
     "rp_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBwdIO), _vp]),
     "rp_step_check": (ctypes.c_int, [ctypes.POINTER(StepArgs)]),
     "rp_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _vp]),
+    "rp_mixer_out_check": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs)]),
+    "rp_mixer_out_work_bytes": (_i64, [ctypes.POINTER(MixerOutArgs)]),
+    "rp_mixer_out_fwd": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs), _vp]),
+    "rp_mixer_out_bwd": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs),
+                                        ctypes.POINTER(MixerOutGrad), _vp]),
 }
 
 _LIB = None

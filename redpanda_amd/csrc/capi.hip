@@ -3,6 +3,7 @@
 // exceptions; failures return a negative status and set a thread-local
 // message (rp_last_error).
 
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -435,6 +436,190 @@ int rp_step(const rp_step_args* a, void* stream) {
   }
   hipError_t e = rp::launch_step(S, NPL, gk, tile, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "step launch");
+  return RP_OK;
+}
+
+}  // extern "C"
+
+// ── mixer output gate ──
+
+namespace {
+
+struct MixPlan {
+  int64_t rows, rows_per_unit;
+  int units, vec;
+};
+
+// Row units (each with its own dD partial): enough workgroups, with the
+// channel tiles, to fill the chip a few times over.  A fixed function of the
+// shape and path, so dD sums the same partials in the same order every call.
+MixPlan mixer_plan(const rp_mixer_out_args* a, bool vec, int workgroups) {
+  MixPlan m{};
+  m.vec = vec ? 1 : 0;
+  m.rows = a->B * a->L;
+  if (m.rows == 0 || a->D == 0) return m;
+  const int64_t tile = vec ? rp::kMixTile : rp::kThreads;
+  const int64_t ctiles = (a->D + tile - 1) / tile;
+  int64_t units = (workgroups + ctiles - 1) / ctiles;
+  units = units < 1 ? 1 : (units > m.rows ? m.rows : units);
+  m.rows_per_unit = (m.rows + units - 1) / units;
+  m.units = (int)((m.rows + m.rows_per_unit - 1) / m.rows_per_unit);
+  return m;
+}
+
+// Whether every row of every operand starts on 16 bytes, so that a lane can
+// move 8 channels of each with one or two 16-byte accesses.
+bool mixer_vec_ok(const rp_mixer_out_args* a, const rp_mixer_out_grad* g) {
+  if (a->D % rp::kMixVec != 0) return false;
+  const int64_t qu = 16 / elem_size(a->dtype_u), qz = 16 / elem_size(a->dtype_z);
+  if (a->u_sb % qu || a->u_sl % qu || a->z_sb % qz || a->z_sl % qz) return false;
+  const void* ptrs[] = {a->y, a->u, a->z, a->Dskip, a->out};
+  for (const void* q : ptrs)
+    if (q && !aligned(q, 16)) return false;
+  if (g != nullptr) {
+    const void* gp[] = {g->dout, g->dy, g->du, g->dz};
+    for (const void* q : gp)
+      if (!aligned(q, 16)) return false;
+  }
+  return true;
+}
+
+rp::MixerOutParams mixer_params(const rp_mixer_out_args* a, const MixPlan& m) {
+  rp::MixerOutParams p{};
+  p.rows = m.rows;
+  p.L = (int)a->L;
+  p.D = (int)a->D;
+  p.k_skip = a->k_skip;
+  p.dt_u = a->dtype_u;
+  p.dt_z = a->dtype_z;
+  p.y = a->y;
+  p.u = a->u;
+  p.usb = a->u_sb;
+  p.usl = a->u_sl;
+  p.z = a->z;
+  p.zsb = a->z_sb;
+  p.zsl = a->z_sl;
+  p.Dskip = a->Dskip;
+  p.out = a->out;
+  p.rows_per_unit = m.rows_per_unit;
+  p.units = m.units;
+  p.vec = m.vec;
+  return p;
+}
+
+// Byte span of a (B, L, D) view with the given strides (elements) and size.
+int64_t span_bytes(const rp_mixer_out_args* a, int64_t sb, int64_t sl, int64_t es) {
+  return ((a->B - 1) * sb + (a->L - 1) * sl + a->D) * es;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rp_mixer_out_check(const rp_mixer_out_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "mixer out args: NULL");
+  if (a->B < 0 || a->L < 0 || a->D < 0)
+    return fail(RP_ERR_INVALID, "mixer out args: negative size");
+  if (a->B > kI32Max || a->L > kI32Max || a->D > kI32Max)
+    return fail(RP_ERR_UNSUPPORTED, "mixer out args: B, L, D must each fit in int32");
+  if (a->k_skip != 1 && a->k_skip != 2)
+    return fail(RP_ERR_INVALID, "mixer out args: k_skip must be 1 or 2");
+  const int codes[2] = {a->dtype_u, a->dtype_z};
+  for (int code : codes)
+    if (code != RP_F32 && code != RP_BF16 && code != RP_F16)
+      return fail(RP_ERR_INVALID, "mixer out args: unknown dtype code %d", code);
+  if (a->reserved != 0) return fail(RP_ERR_INVALID, "mixer out args: reserved field must be 0");
+  if (a->B * a->L == 0 || a->D == 0) return RP_OK;
+  if (!a->y || !a->u || !a->z || !a->Dskip)
+    return fail(RP_ERR_INVALID, "mixer out args: NULL y/u/z/Dskip");
+  if (!aligned(a->y, 4) || !aligned(a->Dskip, 4) || !aligned(a->out, 4) ||
+      !aligned(a->u, elem_size(a->dtype_u)) || !aligned(a->z, elem_size(a->dtype_z)))
+    return fail(RP_ERR_INVALID, "mixer out args: misaligned pointer");
+  if (a->u_sb < 0 || a->u_sl < 0 || a->z_sb < 0 || a->z_sl < 0)
+    return fail(RP_ERR_INVALID, "mixer out args: negative stride");
+  // out is written once per element after that element's inputs are read:
+  // it may be y itself, but must not overlap u or z
+  if (a->out == nullptr) return RP_OK;  // the backward reads no out
+  const int64_t dense = a->B * a->L * a->D * 4;
+  if (overlaps(a->out, dense, a->u, span_bytes(a, a->u_sb, a->u_sl, elem_size(a->dtype_u))) ||
+      overlaps(a->out, dense, a->z, span_bytes(a, a->z_sb, a->z_sl, elem_size(a->dtype_z))))
+    return fail(RP_ERR_INVALID, "mixer out args: out overlaps u or z");
+  if (a->out != a->y && overlaps(a->out, dense, a->y, dense))
+    return fail(RP_ERR_INVALID, "mixer out args: out partly overlaps y");
+  return RP_OK;
+}
+
+int64_t rp_mixer_out_work_bytes(const rp_mixer_out_args* a) {
+  if (rp_mixer_out_check(a) != RP_OK) return -1;
+  // enough for either path (the backward picks one from its pointers too)
+  const int64_t units = std::max(mixer_plan(a, true, rp::kMixerBwdWorkgroups).units,
+                                 mixer_plan(a, false, rp::kMixerBwdWorkgroups).units);
+  return round_up(units * a->D * (int64_t)sizeof(double), 256);
+}
+
+int rp_mixer_out_fwd(const rp_mixer_out_args* a, void* stream) {
+  int st = rp_mixer_out_check(a);
+  if (st != RP_OK) return st;
+  const MixPlan m = mixer_plan(a, mixer_vec_ok(a, nullptr), rp::kMixerFwdWorkgroups);
+  if (m.units == 0) return RP_OK;
+  if (a->out == nullptr) return fail(RP_ERR_INVALID, "mixer out fwd: NULL out");
+  hipError_t e = rp::launch_mixer_out_fwd(mixer_params(a, m), (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "mixer out fwd launch");
+  return RP_OK;
+}
+
+int rp_mixer_out_bwd(const rp_mixer_out_args* a, const rp_mixer_out_grad* g, void* stream) {
+  int st = rp_mixer_out_check(a);
+  if (st != RP_OK) return st;
+  if (g == nullptr) return fail(RP_ERR_INVALID, "mixer out grad: NULL");
+  if (a->D == 0) return RP_OK;
+  if (!g->dD || !aligned(g->dD, 4)) return fail(RP_ERR_INVALID, "mixer out grad: NULL or misaligned dD");
+  rp::MixerOutGrad mg{};
+  mg.dD = g->dD;
+  if (a->B * a->L == 0) {
+    const MixPlan m = mixer_plan(a, false, rp::kMixerBwdWorkgroups);
+    // no rows: dD is a sum over nothing (written by a kernel, so that the
+    // call stays capturable)
+    hipError_t e = rp::launch_mixer_out_bwd(mixer_params(a, m), mg, (hipStream_t)stream);
+    if (e != hipSuccess) return fail_hip(e, "mixer out bwd launch");
+    return RP_OK;
+  }
+  if (!g->dout || !g->dy || !g->du || !g->dz)
+    return fail(RP_ERR_INVALID, "mixer out grad: NULL dout/dy/du/dz");
+  if (!aligned(g->dout, 4) || !aligned(g->dy, 4) || !aligned(g->du, elem_size(a->dtype_u)) ||
+      !aligned(g->dz, elem_size(a->dtype_z)))
+    return fail(RP_ERR_INVALID, "mixer out grad: misaligned pointer");
+  const int64_t n = a->B * a->L * a->D;
+  const int64_t ubytes = span_bytes(a, a->u_sb, a->u_sl, elem_size(a->dtype_u));
+  const int64_t zbytes = span_bytes(a, a->z_sb, a->z_sl, elem_size(a->dtype_z));
+  struct Span { const void* p; int64_t n; };
+  // outputs: disjoint from each other and from every input (dy may be dout itself)
+  const Span outs[4] = {{g->dy, n * 4}, {g->du, n * elem_size(a->dtype_u)},
+                        {g->dz, n * elem_size(a->dtype_z)}, {g->dD, a->D * 4}};
+  const Span ins[5] = {{a->y, n * 4}, {a->u, ubytes}, {a->z, zbytes}, {a->Dskip, a->D * 4},
+                       {g->dout, n * 4}};
+  for (int i = 0; i < 4; ++i) {
+    for (int j = i + 1; j < 4; ++j)
+      if (overlaps(outs[i].p, outs[i].n, outs[j].p, outs[j].n))
+        return fail(RP_ERR_INVALID, "mixer out grad: outputs overlap");
+    for (int j = 0; j < 5; ++j) {
+      if (i == 0 && j == 4 && g->dy == g->dout) continue;
+      if (overlaps(outs[i].p, outs[i].n, ins[j].p, ins[j].n))
+        return fail(RP_ERR_INVALID, "mixer out grad: an output overlaps an input");
+    }
+  }
+  const MixPlan m = mixer_plan(a, mixer_vec_ok(a, g), rp::kMixerBwdWorkgroups);
+  const int64_t need = rp_mixer_out_work_bytes(a);
+  if (g->work == nullptr || g->work_bytes < need || !aligned(g->work, 256))
+    return fail(RP_ERR_WORKSPACE, "mixer out bwd: workspace needs %lld bytes (256-aligned), got %lld",
+                (long long)need, (long long)g->work_bytes);
+  mg.dout = g->dout;
+  mg.dy = g->dy;
+  mg.du = g->du;
+  mg.dz = g->dz;
+  mg.part = static_cast<double*>(g->work);
+  hipError_t e = rp::launch_mixer_out_bwd(mixer_params(a, m), mg, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "mixer out bwd launch");
   return RP_OK;
 }
 

@@ -81,6 +81,47 @@ struct StepParams {
   int rgroups;  // tile kernel: ceil(R / ri)
 };
 
+// The mixer output gate out = (y + k u D) silu(z) over rows = B * L.
+// Rows are split into row groups (units) of rows_per_unit consecutive rows,
+// one workgroup per group and channel tile, each with its own dD partial.
+struct MixerOutParams {
+  int64_t rows;            // B * L
+  int L, D;
+  int k_skip;              // 1 or 2 D-skips
+  int dt_u, dt_z;
+  const float* y;          // (rows, D) fp32
+  const void* u;
+  int64_t usb, usl;
+  const void* z;
+  int64_t zsb, zsl;
+  const float* Dskip;      // (D,)
+  float* out;              // (rows, D) fp32
+  int64_t rows_per_unit;
+  int units;
+  int vec;                 // 1: 16-byte vectors of 8 channels per lane
+};
+
+struct MixerOutGrad {
+  const float* dout;  // (rows, D) fp32
+  float* dy;          // (rows, D) fp32
+  void* du;           // (rows, D) in u's dtype
+  void* dz;           // (rows, D) in z's dtype
+  float* dD;          // (D,)
+  double* part;       // (units, D) workspace; unused when there are no rows
+};
+
+// Workgroups a mixer-output launch aims for (channel tiles x row groups):
+// the forward streams with a few per CU; the backward (about 130 VGPRs on
+// the vector path, 3 workgroups per CU) with one resident round.
+constexpr int kMixerFwdWorkgroups = 1024;
+constexpr int kMixerBwdWorkgroups = 768;
+// Channels per lane on the vector path, and per workgroup column tile.
+constexpr int kMixVec = 8;
+constexpr int kMixTile = kWave * kMixVec;
+
+hipError_t launch_mixer_out_fwd(const MixerOutParams& p, hipStream_t st);
+hipError_t launch_mixer_out_bwd(const MixerOutParams& p, const MixerOutGrad& g, hipStream_t st);
+
 // Channels (one per thread) of the step tile kernel's workgroup, and the
 // most rollouts one of its workgroups walks.
 constexpr int kStepTile = kThreads;

@@ -33,6 +33,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 import torch.utils.checkpoint
 
+from redpanda_amd.mixer import hip_mixer_out
 from redpanda_amd.scan import hip_scan_with_state, hip_trapezoidal_scan
 from redpanda_amd.step import hip_step
 
@@ -164,19 +165,26 @@ class Mamba3Block(nn.Module):
         B/C contracted over the MIMO dimension first (:336-337).  With
         `bidirectional` the fused two-direction scan returns
         S(u) + flip(S(flip(u))) and the skip is added once per direction."""
+        if return_state:
+            y, state = self._scan_core(u, delta, A_real, A_imag, B, C, return_state=True)
+            return y + u * D, state
+        y = self._scan_core(u, delta, A_real, A_imag, B, C, bidirectional=bidirectional)
+        if bidirectional:
+            return y + u * D + u * D
+        return y + u * D
+
+    def _scan_core(self, u, delta, A_real, A_imag, B, C, return_state=False,
+                   bidirectional=False):
+        """The scan alone (no D-skip): y, or (y, (h_last, beta_last))."""
         _need_device(u, "the selective scan")
         cfg = self.config
         Bc = B.sum(dim=-1)
         Cc = C.sum(dim=-1)
         track = self._track_or_none()
         if return_state:
-            y, state = hip_scan_with_state(delta, u, Bc, Cc, A_real, A_imag, track)
-            return y + u * D, state
-        y = hip_trapezoidal_scan(delta, u, Bc, Cc, A_real, A_imag, track,
-                                 cfg.n_rot_state, cfg.d_state, bidirectional=bidirectional)
-        if bidirectional:
-            return y + u * D + u * D
-        return y + u * D
+            return hip_scan_with_state(delta, u, Bc, Cc, A_real, A_imag, track)
+        return hip_trapezoidal_scan(delta, u, Bc, Cc, A_real, A_imag, track,
+                                    cfg.n_rot_state, cfg.d_state, bidirectional=bidirectional)
 
     def ssm(self, u, return_state=False):
         delta, B, C = self._ssm_proj(u)
@@ -185,21 +193,24 @@ class Mamba3Block(nn.Module):
                                                 return_state=return_state)
 
     def forward(self, x):
-        """engine/mamba.py:231-267; the bidirectional branch is one fused launch."""
+        """engine/mamba.py:231-267; the bidirectional branch is one fused launch,
+        and the D-skip and silu(z) gate one fused pass after it."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
         delta, B, C = self._ssm_proj(x_branch)
         A_real, A_imag = self._compute_A()
-        y = self._selective_scan_trapezoidal(x_branch, delta, A_real, A_imag, B, C, self.D,
-                                             bidirectional=self.config.bidirectional)
-        return self.out_proj(y * F.silu(z))
+        bi = self.config.bidirectional
+        y = self._scan_core(x_branch, delta, A_real, A_imag, B, C, bidirectional=bi)
+        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 2 if bi else 1))
 
     def forward_with_state(self, x):
         """engine/mamba.py:269-282: output plus the final (h, beta) cache."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        y, state = self.ssm(x_branch, return_state=True)
-        return self.out_proj(y * F.silu(z)), state
+        delta, B, C = self._ssm_proj(x_branch)
+        A_real, A_imag = self._compute_A()
+        y, state = self._scan_core(x_branch, delta, A_real, A_imag, B, C, return_state=True)
+        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1)), state
 
     # ── O(1) step (engine/mamba.py:427-498) ──
 

@@ -178,7 +178,9 @@ def _header_struct_fields(name):
 @pytest.mark.parametrize("cname,pyname", [("rp_scan_args", "ScanArgs"),
                                           ("rp_scan_fwd_out", "ScanFwdOut"),
                                           ("rp_scan_bwd_io", "ScanBwdIO"),
-                                          ("rp_step_args", "StepArgs")])
+                                          ("rp_step_args", "StepArgs"),
+                                          ("rp_mixer_out_args", "MixerOutArgs"),
+                                          ("rp_mixer_out_grad", "MixerOutGrad")])
 def test_ctypes_structs_mirror_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
     assert py == _header_struct_fields(cname)
@@ -197,3 +199,67 @@ def test_triton_scan_module_names():
     assert params[:9] == ["delta", "u", "B_contracted", "C_contracted", "A_real", "A_imag",
                           "track", "n_rot", "n_state"]
     assert list(inspect.signature(triton_scan.verify).parameters) == ["device", "thorough", "verbose"]
+
+
+def _mixer_args(**kw):
+    a = _lib.MixerOutArgs()
+    a.B, a.L, a.D, a.k_skip = 4, 64, 320, 2
+    a.dtype_u, a.dtype_z = _lib.RP_BF16, _lib.RP_BF16
+    n = 4 * 64 * 320
+    a.y, a.out = 0x1000000, 0x2000000
+    a.u, a.u_sb, a.u_sl = 0x3000000, 64 * 320, 320
+    # z: the second half of an in_proj output of width 640
+    a.z, a.z_sb, a.z_sl = 0x4000000 + 320 * 2, 64 * 640, 640
+    a.Dskip = 0x5000000
+    assert n * 4 < 0x1000000
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_mixer_out_check(lib):
+    chk = lambda **kw: lib.rp_mixer_out_check(ctypes.byref(_mixer_args(**kw)))
+    assert chk() == 0
+    assert chk(out=0x1000000) == 0  # in place over y
+    assert chk(k_skip=3) < 0 and "k_skip" in lib.rp_last_error().decode()
+    assert chk(dtype_z=7) < 0
+    assert chk(reserved=1) < 0
+    assert chk(z=None) < 0
+    assert chk(out=None) == 0  # the backward's arguments carry no out
+    assert lib.rp_mixer_out_fwd(ctypes.byref(_mixer_args(out=None)), None) < 0
+    assert "NULL out" in lib.rp_last_error().decode()
+    assert chk(u=0x3000001) < 0 and "misaligned" in lib.rp_last_error().decode()
+    assert chk(u_sl=-1) < 0
+    assert chk(out=0x3000000 + 64) < 0 and "overlaps" in lib.rp_last_error().decode()
+    assert chk(out=0x1000000 + 4) < 0  # partly over y
+    assert chk(D=1 << 31) < 0
+    # nothing to do: no pointers needed
+    assert chk(B=0, y=None, u=None, z=None, Dskip=None, out=None) == 0
+
+
+def test_mixer_out_workspace(lib):
+    a = _mixer_args()
+    wb = lib.rp_mixer_out_work_bytes(ctypes.byref(a))
+    assert wb > 0 and wb % 256 == 0
+    # row groups x channels float64 partials; a fixed function of the shape
+    assert wb >= 320 * 8 and wb == lib.rp_mixer_out_work_bytes(ctypes.byref(_mixer_args()))
+    assert lib.rp_mixer_out_work_bytes(ctypes.byref(_mixer_args(k_skip=0))) < 0
+
+
+def test_mixer_out_bwd_rules(lib):
+    a = _mixer_args(dtype_u=_lib.RP_F32, dtype_z=_lib.RP_F32, z_sb=64 * 320, z_sl=320,
+                    z=0x4000000)
+    n = 4 * 64 * 320 * 4
+    wb = lib.rp_mixer_out_work_bytes(ctypes.byref(a))
+    base = dict(dout=0x6000000, dy=0x7000000, du=0x8000000, dz=0x9000000, dD=0xa000000,
+                work=0xb000000, work_bytes=wb)
+    bwd = lambda **kw: lib.rp_mixer_out_bwd(ctypes.byref(a), ctypes.byref(
+        _lib.MixerOutGrad(**{**base, **kw})), None)
+    # each failure below is caught on the host, before any launch
+    assert bwd(work_bytes=wb - 8) == -4
+    assert bwd(work=0xb000000 + 16) == -4
+    assert bwd(du=0x9000000 + 128) < 0 and "overlap" in lib.rp_last_error().decode()
+    assert bwd(dz=0x3000000) < 0 and "overlaps an input" in lib.rp_last_error().decode()
+    assert bwd(dD=None) < 0
+    assert bwd(dy=None) < 0
+    assert n < 0x1000000
