@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 3
+#define RP_ABI_VERSION 4
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -199,6 +199,59 @@ int rp_mixer_out_fwd(const rp_mixer_out_args* a, void* stream);
 
 /* The autograd of those ops in one pass (plus a small dD reduction). */
 int rp_mixer_out_bwd(const rp_mixer_out_args* a, const rp_mixer_out_grad* g, void* stream);
+
+/*
+ * The SSM input prologue (engine/mamba.py:297-300 BCNorm, :89 RMSNorm,
+ * :336-337 contraction over p): per token, Bc[n] = sum_p RMSNorm(B_raw)[n,p]
+ * and the same for C, or the plain sums over p when normalize = 0.
+ * B_raw, C_raw: (T, N*P) with row strides B_sr, C_sr (elements), inner
+ * stride 1, one dtype for both (RP_F32 / RP_BF16 / RP_F16; they are views
+ * of one x_proj output); wB, wC: (N*P,) fp32 norm weights; Bc, Cc: (T, N)
+ * fp32 contiguous.  1 <= N <= RP_MAX_STATE, 1 <= P <= 8.
+ */
+typedef struct rp_bcnorm_args {
+  int64_t T, N, P;
+  int32_t dtype_x;
+  int32_t normalize;       /* 0 or 1 */
+  float eps;
+  int32_t reserved;        /* must be 0 */
+  const void* B_raw;  int64_t B_sr;
+  const void* C_raw;  int64_t C_sr;
+  const float* wB;
+  const float* wC;
+  float* Bc;
+  float* Cc;
+} rp_bcnorm_args;
+
+/*
+ * Its backward given dBc, dCc (T, N) fp32: dB_raw, dC_raw (T, N*P)
+ * contiguous in dtype_x; dwB, dwC (N*P,) fp32 (deterministic sums; unused
+ * when normalize = 0).  work: rp_bcnorm_work_bytes() of scratch.
+ */
+typedef struct rp_bcnorm_grad {
+  const float* dBc;
+  const float* dCc;
+  void* dB_raw;
+  void* dC_raw;
+  float* dwB;
+  float* dwC;
+  void* work;
+  int64_t work_bytes;
+} rp_bcnorm_grad;
+
+/* Validate BCNorm arguments on the host without launching anything. */
+int rp_bcnorm_check(const rp_bcnorm_args* a);
+
+/* Bytes of scratch rp_bcnorm_bwd needs. */
+int64_t rp_bcnorm_work_bytes(const rp_bcnorm_args* a);
+
+/* Bc, Cc from the raw projections; replaces Mamba3Block._ssm_proj's BCNorm
+ * and the B/C sums of _selective_scan_trapezoidal (engine/mamba.py:297-300,
+ * :336-337) and of step (:470-471). */
+int rp_bcnorm_fwd(const rp_bcnorm_args* a, void* stream);
+
+/* The autograd of those ops in one pass (plus a small dw reduction). */
+int rp_bcnorm_bwd(const rp_bcnorm_args* a, const rp_bcnorm_grad* g, void* stream);
 
 /* ABI version this library was built with (RP_ABI_VERSION). */
 int rp_abi_version(void);

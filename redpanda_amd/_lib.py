@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -76,6 +76,22 @@ class MixerOutGrad(ctypes.Structure):
     ]
 
 
+class BcNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("T", _i64), ("N", _i64), ("P", _i64),
+        ("dtype_x", _i32), ("normalize", _i32), ("eps", ctypes.c_float), ("reserved", _i32),
+        ("B_raw", _vp), ("B_sr", _i64), ("C_raw", _vp), ("C_sr", _i64),
+        ("wB", _vp), ("wC", _vp), ("Bc", _vp), ("Cc", _vp),
+    ]
+
+
+class BcNormGrad(ctypes.Structure):
+    _fields_ = [
+        ("dBc", _vp), ("dCc", _vp), ("dB_raw", _vp), ("dC_raw", _vp),
+        ("dwB", _vp), ("dwC", _vp), ("work", _vp), ("work_bytes", _i64),
+    ]
+
+
 # Every symbol include/redpanda_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "rp_abi_version": (ctypes.c_int, []),
@@ -87,6 +103,10 @@ SIGNATURES = {
     "rp_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBwdIO), _vp]),
     "rp_step_check": (ctypes.c_int, [ctypes.POINTER(StepArgs)]),
     "rp_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _vp]),
+    "rp_bcnorm_check": (ctypes.c_int, [ctypes.POINTER(BcNormArgs)]),
+    "rp_bcnorm_work_bytes": (_i64, [ctypes.POINTER(BcNormArgs)]),
+    "rp_bcnorm_fwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), _vp]),
+    "rp_bcnorm_bwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), ctypes.POINTER(BcNormGrad), _vp]),
     "rp_mixer_out_check": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs)]),
     "rp_mixer_out_work_bytes": (_i64, [ctypes.POINTER(MixerOutArgs)]),
     "rp_mixer_out_fwd": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs), _vp]),

@@ -624,3 +624,130 @@ int rp_mixer_out_bwd(const rp_mixer_out_args* a, const rp_mixer_out_grad* g, voi
 }
 
 }  // extern "C"
+
+// ── BCNorm + p-sum ──
+
+namespace {
+
+rp::BcNormParams bcnorm_params(const rp_bcnorm_args* a) {
+  rp::BcNormParams p{};
+  p.T = a->T;
+  p.N = (int)a->N;
+  p.P = (int)a->P;
+  p.dt_x = a->dtype_x;
+  p.normalize = a->normalize;
+  p.eps = a->eps;
+  p.x[0] = a->B_raw;
+  p.x[1] = a->C_raw;
+  p.xs[0] = a->B_sr;
+  p.xs[1] = a->C_sr;
+  p.w[0] = a->wB;
+  p.w[1] = a->wC;
+  p.out[0] = a->Bc;
+  p.out[1] = a->Cc;
+  if (a->T > 0) {
+    int64_t tpg = (a->T + rp::kBcNormWorkgroups - 1) / rp::kBcNormWorkgroups;
+    tpg = tpg < rp::kWaves ? rp::kWaves : tpg;
+    p.tokens_per_group = tpg;
+    p.groups = (int)((a->T + tpg - 1) / tpg);
+  }
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rp_bcnorm_check(const rp_bcnorm_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "bcnorm args: NULL");
+  if (a->T < 0 || a->N < 1 || a->P < 1)
+    return fail(RP_ERR_INVALID, "bcnorm args: T >= 0, N >= 1, P >= 1 required");
+  if (a->N > RP_MAX_STATE || a->P > 8)
+    return fail(RP_ERR_UNSUPPORTED, "bcnorm args: N=%lld P=%lld beyond N <= %d, P <= 8",
+                (long long)a->N, (long long)a->P, RP_MAX_STATE);
+  if (a->dtype_x != RP_F32 && a->dtype_x != RP_BF16 && a->dtype_x != RP_F16)
+    return fail(RP_ERR_INVALID, "bcnorm args: unknown dtype code %d", a->dtype_x);
+  if ((a->normalize != 0 && a->normalize != 1) || a->reserved != 0)
+    return fail(RP_ERR_INVALID, "bcnorm args: normalize must be 0 or 1, reserved 0");
+  if (a->normalize && !(a->eps >= 0.f))
+    return fail(RP_ERR_INVALID, "bcnorm args: eps must be >= 0");
+  if (a->normalize && (!a->wB || !a->wC || !aligned(a->wB, 4) || !aligned(a->wC, 4)))
+    return fail(RP_ERR_INVALID, "bcnorm args: normalize needs 4-byte aligned wB, wC");
+  if (a->T == 0) return RP_OK;
+  const int64_t K = a->N * a->P;
+  if (!a->B_raw || !a->C_raw) return fail(RP_ERR_INVALID, "bcnorm args: NULL B_raw/C_raw");
+  if (!aligned(a->B_raw, elem_size(a->dtype_x)) || !aligned(a->C_raw, elem_size(a->dtype_x)) ||
+      (a->Bc && !aligned(a->Bc, 4)) || (a->Cc && !aligned(a->Cc, 4)))
+    return fail(RP_ERR_INVALID, "bcnorm args: misaligned pointer");
+  if (a->B_sr < K || a->C_sr < K)
+    return fail(RP_ERR_INVALID, "bcnorm args: row stride shorter than N*P");
+  return RP_OK;
+}
+
+int64_t rp_bcnorm_work_bytes(const rp_bcnorm_args* a) {
+  if (rp_bcnorm_check(a) != RP_OK) return -1;
+  const rp::BcNormParams p = bcnorm_params(a);
+  return round_up((int64_t)p.groups * 2 * a->N * a->P * (int64_t)sizeof(double), 256);
+}
+
+int rp_bcnorm_fwd(const rp_bcnorm_args* a, void* stream) {
+  int st = rp_bcnorm_check(a);
+  if (st != RP_OK) return st;
+  if (a->T == 0) return RP_OK;
+  if (!a->Bc || !a->Cc) return fail(RP_ERR_INVALID, "bcnorm fwd: NULL Bc/Cc");
+  const int64_t in_b = ((a->T - 1) * a->B_sr + a->N * a->P) * elem_size(a->dtype_x);
+  const int64_t in_c = ((a->T - 1) * a->C_sr + a->N * a->P) * elem_size(a->dtype_x);
+  const int64_t ob = a->T * a->N * 4;
+  if (overlaps(a->Bc, ob, a->Cc, ob) || overlaps(a->Bc, ob, a->B_raw, in_b) ||
+      overlaps(a->Bc, ob, a->C_raw, in_c) || overlaps(a->Cc, ob, a->B_raw, in_b) ||
+      overlaps(a->Cc, ob, a->C_raw, in_c))
+    return fail(RP_ERR_INVALID, "bcnorm fwd: outputs overlap each other or the inputs");
+  hipError_t e = rp::launch_bcnorm_fwd(bcnorm_params(a), (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "bcnorm fwd launch");
+  return RP_OK;
+}
+
+int rp_bcnorm_bwd(const rp_bcnorm_args* a, const rp_bcnorm_grad* g, void* stream) {
+  int st = rp_bcnorm_check(a);
+  if (st != RP_OK) return st;
+  if (g == nullptr) return fail(RP_ERR_INVALID, "bcnorm grad: NULL");
+  if (a->normalize && (!g->dwB || !g->dwC || !aligned(g->dwB, 4) || !aligned(g->dwC, 4)))
+    return fail(RP_ERR_INVALID, "bcnorm grad: normalize needs 4-byte aligned dwB, dwC");
+  const rp::BcNormParams p = bcnorm_params(a);
+  rp::BcNormGrad bg{};
+  bg.dw[0] = g->dwB;
+  bg.dw[1] = g->dwC;
+  if (a->T > 0) {
+    const int64_t K = a->N * a->P, es = elem_size(a->dtype_x);
+    if (!g->dBc || !g->dCc || !g->dB_raw || !g->dC_raw)
+      return fail(RP_ERR_INVALID, "bcnorm grad: NULL dBc/dCc/dB_raw/dC_raw");
+    if (!aligned(g->dBc, 4) || !aligned(g->dCc, 4) || !aligned(g->dB_raw, es) ||
+        !aligned(g->dC_raw, es))
+      return fail(RP_ERR_INVALID, "bcnorm grad: misaligned pointer");
+    const int64_t nx = a->T * K * es;
+    if (overlaps(g->dB_raw, nx, g->dC_raw, nx))
+      return fail(RP_ERR_INVALID, "bcnorm grad: dB_raw and dC_raw overlap");
+    const int64_t in_b = ((a->T - 1) * a->B_sr + K) * es, in_c = ((a->T - 1) * a->C_sr + K) * es;
+    const int64_t gb = a->T * a->N * 4;
+    const void* outs[2] = {g->dB_raw, g->dC_raw};
+    for (const void* o : outs)
+      if (overlaps(o, nx, a->B_raw, in_b) || overlaps(o, nx, a->C_raw, in_c) ||
+          overlaps(o, nx, g->dBc, gb) || overlaps(o, nx, g->dCc, gb))
+        return fail(RP_ERR_INVALID, "bcnorm grad: an output overlaps an input");
+    bg.g[0] = g->dBc;
+    bg.g[1] = g->dCc;
+    bg.dx[0] = g->dB_raw;
+    bg.dx[1] = g->dC_raw;
+  }
+  const int64_t need = rp_bcnorm_work_bytes(a);
+  if (a->normalize && need > 0 &&
+      (g->work == nullptr || g->work_bytes < need || !aligned(g->work, 256)))
+    return fail(RP_ERR_WORKSPACE, "bcnorm bwd: workspace needs %lld bytes (256-aligned), got %lld",
+                (long long)need, (long long)g->work_bytes);
+  bg.part = static_cast<double*>(g->work);
+  hipError_t e = rp::launch_bcnorm_bwd(p, bg, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "bcnorm bwd launch");
+  return RP_OK;
+}
+
+}  // extern "C"

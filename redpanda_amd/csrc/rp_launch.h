@@ -122,6 +122,34 @@ constexpr int kMixTile = kWave * kMixVec;
 hipError_t launch_mixer_out_fwd(const MixerOutParams& p, hipStream_t st);
 hipError_t launch_mixer_out_bwd(const MixerOutParams& p, const MixerOutGrad& g, hipStream_t st);
 
+// BCNorm + MIMO p-sum of the B and C projections (part 0: B, part 1: C).
+struct BcNormParams {
+  int64_t T;               // tokens
+  int N, P;                // states, MIMO channels (K = N * P features)
+  int dt_x;                // storage dtype of both projections
+  int normalize;           // 1: RMSNorm before the p-sum
+  float eps;
+  const void* x[2];        // (T, K), row strides xs, inner stride 1
+  int64_t xs[2];
+  const float* w[2];       // (K,) norm weights
+  float* out[2];           // (T, N) fp32
+  int64_t tokens_per_group;
+  int groups;              // workgroups (token ranges)
+};
+
+struct BcNormGrad {
+  const float* g[2];       // (T, N) fp32
+  void* dx[2];             // (T, K) contiguous, dt_x
+  float* dw[2];            // (K,)
+  double* part;            // (groups, 2, K) workspace
+};
+
+// Workgroups a BCNorm launch aims for.
+constexpr int kBcNormWorkgroups = 1024;
+
+hipError_t launch_bcnorm_fwd(const BcNormParams& p, hipStream_t st);
+hipError_t launch_bcnorm_bwd(const BcNormParams& p, const BcNormGrad& g, hipStream_t st);
+
 // Channels (one per thread) of the step tile kernel's workgroup, and the
 // most rollouts one of its workgroups walks.
 constexpr int kStepTile = kThreads;

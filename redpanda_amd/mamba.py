@@ -33,6 +33,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 import torch.utils.checkpoint
 
+from redpanda_amd.bcnorm import hip_bcnorm_psum
 from redpanda_amd.mixer import hip_mixer_out
 from redpanda_amd.scan import hip_scan_with_state, hip_trapezoidal_scan
 from redpanda_amd.step import hip_step
@@ -157,6 +158,21 @@ class Mamba3Block(nn.Module):
         delta = F.softplus(self.dt_proj(dt_raw))
         return delta, B_raw.view(*lead, n, p), C_raw.view(*lead, n, p)
 
+    def _ssm_proj_contracted(self, u):
+        """(delta, Bc, Cc): _ssm_proj followed by the sums over p
+        (engine/mamba.py:336-337), with BCNorm and the sums in one fused
+        kernel; Bc, Cc fp32 (..., d_state)."""
+        cfg = self.config
+        n, p = cfg.d_state, cfg.mimo_p
+        dt_raw, B_raw, C_raw = self.x_proj(u).split([cfg.dt_rank, n * p, n * p], dim=-1)
+        if cfg.use_bcnorm:
+            Bc, Cc = hip_bcnorm_psum(B_raw, C_raw, self.b_norm.weight, self.c_norm.weight, p,
+                                     self.b_norm.eps)
+        else:
+            Bc, Cc = hip_bcnorm_psum(B_raw, C_raw, None, None, p, normalize=False)
+        delta = F.softplus(self.dt_proj(dt_raw))
+        return delta, Bc, Cc
+
     # ── scan ──
 
     def _selective_scan_trapezoidal(self, u, delta, A_real, A_imag, B, C, D,
@@ -174,12 +190,13 @@ class Mamba3Block(nn.Module):
         return y + u * D
 
     def _scan_core(self, u, delta, A_real, A_imag, B, C, return_state=False,
-                   bidirectional=False):
-        """The scan alone (no D-skip): y, or (y, (h_last, beta_last))."""
+                   bidirectional=False, contracted=False):
+        """The scan alone (no D-skip): y, or (y, (h_last, beta_last)).  B, C:
+        (..., n, p), or already contracted (..., n) with contracted=True."""
         _need_device(u, "the selective scan")
         cfg = self.config
-        Bc = B.sum(dim=-1)
-        Cc = C.sum(dim=-1)
+        Bc = B if contracted else B.sum(dim=-1)
+        Cc = C if contracted else C.sum(dim=-1)
         track = self._track_or_none()
         if return_state:
             return hip_scan_with_state(delta, u, Bc, Cc, A_real, A_imag, track)
@@ -197,19 +214,21 @@ class Mamba3Block(nn.Module):
         and the D-skip and silu(z) gate one fused pass after it."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        delta, B, C = self._ssm_proj(x_branch)
+        delta, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
         bi = self.config.bidirectional
-        y = self._scan_core(x_branch, delta, A_real, A_imag, B, C, bidirectional=bi)
+        y = self._scan_core(x_branch, delta, A_real, A_imag, Bc, Cc, bidirectional=bi,
+                            contracted=True)
         return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 2 if bi else 1))
 
     def forward_with_state(self, x):
         """engine/mamba.py:269-282: output plus the final (h, beta) cache."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        delta, B, C = self._ssm_proj(x_branch)
+        delta, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
-        y, state = self._scan_core(x_branch, delta, A_real, A_imag, B, C, return_state=True)
+        y, state = self._scan_core(x_branch, delta, A_real, A_imag, Bc, Cc, return_state=True,
+                                   contracted=True)
         return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1)), state
 
     # ── O(1) step (engine/mamba.py:427-498) ──
@@ -221,11 +240,9 @@ class Mamba3Block(nn.Module):
         cfg = self.config
         x_branch, z = self.in_proj(x_t).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        delta, B_mat, C_mat = self._ssm_proj(x_branch)
+        delta, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
         track = self._track_or_none()
-        Bc = B_mat.sum(dim=-1)
-        Cc = C_mat.sum(dim=-1)
         grad = torch.is_grad_enabled() and (
             any(p.requires_grad for p in self.parameters()) or x_t.requires_grad or
             (state is not None and any(s.requires_grad for s in state)))

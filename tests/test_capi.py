@@ -180,7 +180,9 @@ def _header_struct_fields(name):
                                           ("rp_scan_bwd_io", "ScanBwdIO"),
                                           ("rp_step_args", "StepArgs"),
                                           ("rp_mixer_out_args", "MixerOutArgs"),
-                                          ("rp_mixer_out_grad", "MixerOutGrad")])
+                                          ("rp_mixer_out_grad", "MixerOutGrad"),
+                                          ("rp_bcnorm_args", "BcNormArgs"),
+                                          ("rp_bcnorm_grad", "BcNormGrad")])
 def test_ctypes_structs_mirror_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
     assert py == _header_struct_fields(cname)
@@ -263,3 +265,43 @@ def test_mixer_out_bwd_rules(lib):
     assert bwd(dD=None) < 0
     assert bwd(dy=None) < 0
     assert n < 0x1000000
+
+
+def _bcnorm_args(**kw):
+    a = _lib.BcNormArgs()
+    a.T, a.N, a.P = 1000, 40, 4
+    a.dtype_x, a.normalize, a.eps = _lib.RP_BF16, 1, 1e-5
+    a.B_raw, a.B_sr = 0x1000000 + 2 * 7, 7 + 320
+    a.C_raw, a.C_sr = 0x1000000 + 2 * (7 + 160), 7 + 320
+    a.wB, a.wC = 0x2000000, 0x2001000
+    a.Bc, a.Cc = 0x3000000, 0x3100000
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_bcnorm_check(lib):
+    chk = lambda **kw: lib.rp_bcnorm_check(ctypes.byref(_bcnorm_args(**kw)))
+    assert chk() == 0
+    assert chk(P=9) == -2 and chk(N=129) == -2
+    assert chk(N=0) < 0 and chk(T=-1) < 0
+    assert chk(dtype_x=5) < 0
+    assert chk(normalize=2) < 0 and chk(reserved=1) < 0
+    assert chk(wB=None) < 0 and "wB" in lib.rp_last_error().decode()
+    assert chk(normalize=0, wB=None, wC=None) == 0  # plain p-sum: no weights
+    assert chk(B_sr=100) < 0 and "row stride" in lib.rp_last_error().decode()
+    assert chk(B_raw=0x1000001) < 0
+    assert chk(eps=-1.0) < 0
+    assert chk(T=0, B_raw=None, C_raw=None) == 0
+    # outputs over an input are refused before any launch
+    assert lib.rp_bcnorm_fwd(ctypes.byref(_bcnorm_args(Bc=0x1000000)), None) < 0
+    assert "overlap" in lib.rp_last_error().decode()
+
+
+def test_bcnorm_workspace(lib):
+    a = _bcnorm_args()
+    wb = lib.rp_bcnorm_work_bytes(ctypes.byref(a))
+    assert wb > 0 and wb % 256 == 0 and wb >= 2 * 160 * 8
+    g = _lib.BcNormGrad(dBc=0x4000000, dCc=0x4100000, dB_raw=0x5000000, dC_raw=0x5200000,
+                        dwB=0x6000000, dwC=0x6001000, work=0x7000000, work_bytes=wb - 256)
+    assert lib.rp_bcnorm_bwd(ctypes.byref(a), ctypes.byref(g), None) == -4

@@ -192,8 +192,9 @@ def test_in_place_over_y(gpu_lib):
 
 
 def test_block_forward_uses_fused_gate(gpu_lib):
-    """Mamba3Block.forward (fused gate) against the block's scan + the eager
-    gate, causal and bidirectional, output and parameter gradients."""
+    """Mamba3Block.forward (fused prologue and gate) against the block's
+    scan with the eager prologue and gate, causal and bidirectional, output
+    and parameter gradients (norm-wise per tensor)."""
     from redpanda_amd import mamba as hm
 
     for bi in (False, True):
@@ -219,7 +220,10 @@ def test_block_forward_uses_fused_gate(gpu_lib):
         ref = eager_block(x)
         ref.square().sum().backward()
         torch.cuda.synchronize()
-        _close(out, ref, 1e-5, f"block out bi={bi}")
+        # norm-wise: the block's B/C prologue is fused too, so the scan's
+        # inputs differ from the eager block's in the last bits
+        d = (out - ref).abs().max() / ref.abs().max()
+        assert float(d) <= 1e-5, f"block out bi={bi}: {float(d):.2e}"
         for k, p in blk.named_parameters():
             d = (g_fused[k] - p.grad).abs().max() / (p.grad.abs().max() + 1e-30)
             assert float(d) <= 1e-5, f"grad {k} bi={bi}: {float(d):.2e}"
