@@ -20,6 +20,8 @@ Besides the headline number the JSON line carries:
   kernels       the same for every kernel of the path;
   long_sequence tokens/s of a causal fwd + bwd at L=2048, d_state 72;
   step          rollout-steps/s of the fused step kernel over 8 layers;
+  layer         tokens/s of a whole bidirectional Mamba3Block fwd + bwd, fused,
+                beside the reference's layer with only its scan swapped;
   mixer_gate    the fused (y + 2 u D) silu(z) gate after the scan: kernel
                 durations and bytes, and fwd + bwd against torch's ops;
   cpu_baseline  the reference's CPU PyTorch path (the oracle's fp32
@@ -369,6 +371,67 @@ def bench_mixer(torch, args):
                 t_torch=t_torch)
 
 
+# One Eval-Mamba layer: d_model 768 (d_inner 1536), d_state 32 + 8, mimo_p 4,
+# bidirectional, at the scan shape's batch and length, under bf16 autocast.
+LAYER_SHAPE = dict(B=256, L=64, d_model=768, d_state=40, n_track=8)
+
+
+def bench_layer(torch, args):
+    """Forward + backward of one bidirectional Mamba3Block: the fused module,
+    against the reference's own op sequence for the layer (engine/mamba.py:
+    231-267, 284-301, 318-350) with only the scan call swapped for the HIP
+    scan, i.e. the one-file drop-in of engine/triton_scan.py."""
+    import torch.nn.functional as F
+    from redpanda_amd import mamba as hm
+    from redpanda_amd.scan import hip_trapezoidal_scan
+    sh = LAYER_SHAPE
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = hm.MambaConfig(d_model=sh["d_model"], n_layer=1, d_state=sh["d_state"],
+                         n_track_state=sh["n_track"], bidirectional=True)
+    blk = hm.Mamba3Block(cfg).to(dev)
+    gen = torch.Generator(device=dev).manual_seed(1009)
+    x = torch.randn(sh["B"], sh["L"], sh["d_model"], generator=gen, device=dev)
+    x.requires_grad_(True)
+
+    def scan_only_dropin(xin):
+        # the reference's block with triton_trapezoidal_scan -> HIP scan
+        xb, z = blk.in_proj(xin).chunk(2, dim=-1)
+        xb = F.silu(xb)
+        delta, B, C = blk._ssm_proj(xb)
+        Ar, Ai = blk._compute_A()
+        track = blk._track_gate()
+
+        def scan(u, d, b, c):
+            return hip_trapezoidal_scan(d, u, b.sum(-1), c.sum(-1), Ar, Ai, track,
+                                        cfg.n_rot_state, cfg.d_state) + u * blk.D
+
+        y = scan(xb, delta, B, C)
+        y = y + scan(xb.flip(1), delta.flip(1), B.flip(1), C.flip(1)).flip(1)
+        return blk.out_proj(y * F.silu(z))
+
+    def run(fn):
+        def step():
+            x.grad = None
+            blk.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                out = fn(x)
+            out.float().square().mean().backward()
+        return step
+
+    fused, dropin = run(blk), run(scan_only_dropin)
+    for fn in (fused, dropin):
+        for _ in range(max(args.warmup, 2)):
+            fn()
+    torch.cuda.synchronize()
+    timer = EventTimer(torch)
+    reps = max(5, min(args.steps, 10))
+    t_fused = min(timer.time(fused, reps) for _ in range(2))
+    t_dropin = min(timer.time(dropin, reps) for _ in range(2))
+    T = sh["B"] * sh["L"]
+    return dict(t_fused=t_fused, t_dropin=t_dropin, tok_fused=T / t_fused, tok_dropin=T / t_dropin)
+
+
 def bench_long(torch, args):
     """Causal fwd + bwd at the long-sequence shape, through the C ABI with
     preallocated buffers (inputs generated on the device)."""
@@ -650,6 +713,10 @@ def main():
         lng = bench_long(torch, args)
         print(f"[bench] long: {lng['tok_s']:.4g} tokens/s; fwd {lng['t_fwd'] * 1e3:.2f} ms, "
               f"bwd {lng['t_bwd'] * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    lay = bench_layer(torch, args)
+    print(f"[bench] layer fwd+bwd: fused {lay['t_fused'] * 1e3:.3f} ms "
+          f"({lay['tok_fused']:.4g} tokens/s); scan-only drop-in {lay['t_dropin'] * 1e3:.3f} ms "
+          f"({lay['tok_dropin']:.4g} tokens/s)", file=sys.stderr, flush=True)
     mix = bench_mixer(torch, args)
     print(f"[bench] mixer gate: fwd {mix['t_fwd'] * 1e6:.1f} us "
           f"({mix['fwd_bytes'] / mix['t_fwd'] / 1e9:.0f} GB/s), bwd {mix['t_bwd'] * 1e6:.1f} us "
@@ -723,6 +790,16 @@ def main():
             "fwd_s": lng["t_fwd"], "bwd_s": lng["t_bwd"],
             "alg_bytes_fwd": lng["fwd_bytes"], "alg_bytes_bwd": lng["bwd_bytes"],
         }
+    line["layer"] = {
+        "metric": "tokens/s", "value": lay["tok_fused"],
+        "config": {"workload": "one bidirectional Mamba3Block forward + backward under bf16 "
+                               "autocast (projections on hipBLASLt, SSM path fused HIP)",
+                   **LAYER_SHAPE, "mimo_p": 4},
+        "fwd_bwd_s": lay["t_fused"],
+        "scan_only_dropin": {"workload": "the reference's layer ops with only the scan "
+                                         "swapped for the HIP scan",
+                             "fwd_bwd_s": lay["t_dropin"], "tokens_s": lay["tok_dropin"]},
+    }
     line["mixer_gate"] = {
         "workload": "(y + 2 u D) silu(z) of the bidirectional layer at the scan shape, "
                     "bf16 u / z (z a chunk of the in_proj output), fp32 y and gradients",

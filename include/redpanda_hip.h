@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 4
+#define RP_ABI_VERSION 5
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -55,12 +55,15 @@ enum {
  * tanh(theta) gates, or NULL when NT == 0.  h0, beta0: NULL (zero state, as
  * the reference's scan always starts), or (B, D, N) fp32 contiguous state to
  * continue from — the cache format of step() (causal scans, L >= 1).
+ * delta_softplus = 1: delta holds the dt projection x and the scan runs on
+ * softplus(x) as engine/mamba.py:300 computes it (F.softplus, beta 1,
+ * threshold 20, fp32); rp_scan_bwd's d_delta is then the gradient of x.
  */
 typedef struct rp_scan_args {
   int64_t B, L, D, N, NR, NT;
   int32_t dtype_delta, dtype_u, dtype_B, dtype_C;  /* RP_F32 / RP_BF16 / RP_F16 */
   int32_t bidirectional;   /* 0: causal; 1: y = S(x) + flip(S(flip(x)))     */
-  int32_t reserved;        /* must be 0 */
+  int32_t delta_softplus;  /* 0: delta as given; 1: see below               */
   const void* delta;  int64_t delta_sb, delta_sl;
   const void* u;      int64_t u_sb, u_sl;
   const void* Bc;     int64_t Bc_sb, Bc_sl;
@@ -75,7 +78,8 @@ typedef struct rp_scan_args {
 /*
  * Forward outputs.  y: (B, L, D) fp32 contiguous, WITHOUT the u*D skip
  * (the caller adds it, as engine/mamba.py:350 does).  ckpt: NULL for
- * inference, else rp_scan_ckpt_bytes() of workspace that rp_scan_bwd reads.
+ * inference, else rp_scan_ckpt_bytes() of 256-byte aligned workspace that
+ * rp_scan_bwd reads (with delta_softplus it also keeps softplus(x)).
  * h_last, beta_last: NULL, or (B, D, N) fp32 contiguous to receive the final
  * recurrent state (h_{L-1}, beta_{L-1}) that rp_step continues from
  * (engine/mamba.py:377-379); causal scans only.
@@ -146,7 +150,7 @@ typedef struct rp_step_args {
   float* beta_out;
   float* y;
   int32_t broadcast_state;  /* 0 or 1, see above */
-  int32_t reserved;         /* must be 0 */
+  int32_t delta_softplus;   /* 0 or 1: delta holds x, the step uses softplus(x) */
 } rp_step_args;
 
 /*

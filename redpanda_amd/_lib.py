@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -27,7 +27,7 @@ class ScanArgs(ctypes.Structure):
     _fields_ = [
         ("B", _i64), ("L", _i64), ("D", _i64), ("N", _i64), ("NR", _i64), ("NT", _i64),
         ("dtype_delta", _i32), ("dtype_u", _i32), ("dtype_B", _i32), ("dtype_C", _i32),
-        ("bidirectional", _i32), ("reserved", _i32),
+        ("bidirectional", _i32), ("delta_softplus", _i32),
         ("delta", _vp), ("delta_sb", _i64), ("delta_sl", _i64),
         ("u", _vp), ("u_sb", _i64), ("u_sl", _i64),
         ("Bc", _vp), ("Bc_sb", _i64), ("Bc_sl", _i64),
@@ -56,7 +56,7 @@ class StepArgs(ctypes.Structure):
         ("Bc", _vp), ("Bc_sr", _i64), ("Cc", _vp), ("Cc_sr", _i64),
         ("h_in", _vp), ("beta_in", _vp), ("A_real", _vp), ("A_imag", _vp), ("track", _vp),
         ("Dskip", _vp), ("h_out", _vp), ("beta_out", _vp), ("y", _vp),
-        ("broadcast_state", _i32), ("reserved", _i32),
+        ("broadcast_state", _i32), ("delta_softplus", _i32),
     ]
 
 

@@ -68,6 +68,7 @@ struct Plan {
   int S, NPL, CB, ntiles, nck, ndir, bg, nbg;
   int gk;     // gate kind: rotational / tracking split fixed at compile time
   int64_t ckpt_bytes, part_bc_bytes, part_par_bytes;
+  int64_t dcache_off;  // byte offset of the softplus(x) cache in the workspace, or -1
 };
 
 int scan_validate(const rp_scan_args* a) {
@@ -88,7 +89,8 @@ int scan_validate(const rp_scan_args* a) {
   for (int code : codes)
     if (code != RP_F32 && code != RP_BF16 && code != RP_F16)
       return fail(RP_ERR_INVALID, "scan args: unknown dtype code %d", code);
-  if (a->reserved != 0) return fail(RP_ERR_INVALID, "scan args: reserved field must be 0");
+  if (a->delta_softplus != 0 && a->delta_softplus != 1)
+    return fail(RP_ERR_INVALID, "scan args: delta_softplus must be 0 or 1");
   if (a->bidirectional != 0 && a->bidirectional != 1)
     return fail(RP_ERR_INVALID, "scan args: bidirectional must be 0 or 1");
   const int64_t work = a->B * a->L;
@@ -144,6 +146,13 @@ Plan make_plan(const rp_scan_args* a) {
   pl.bg = (int)bg;
   pl.nbg = (int)((a->B + bg - 1) / bg);
   pl.ckpt_bytes = (int64_t)pl.ndir * a->B * pl.nck * pl.ntiles * rp::kThreads * NPL * 4;
+  // with softplus the forward also keeps delta = softplus(x) for the
+  // backward, which then stages it as stored
+  pl.dcache_off = -1;
+  if (a->delta_softplus && a->B * a->L * a->D > 0) {
+    pl.dcache_off = round_up(pl.ckpt_bytes, 256);
+    pl.ckpt_bytes = pl.dcache_off + a->B * a->L * a->D * 4;
+  }
   pl.part_bc_bytes = round_up(2 * (int64_t)pl.ntiles * a->B * a->L * a->N * 4, 256);
   pl.part_par_bytes = round_up((int64_t)pl.nbg * 2 * a->D * a->N * 8, 256);
   return pl;
@@ -175,6 +184,7 @@ rp::ScanParams scan_params(const rp_scan_args* a, const Plan& pl) {
   p.NR = (int)a->NR;
   p.NT = (int)a->NT;
   p.dt_delta = a->dtype_delta;
+  p.dsp = a->delta_softplus;
   p.dt_u = a->dtype_u;
   p.dt_B = a->dtype_B;
   p.dt_C = a->dtype_C;
@@ -254,8 +264,8 @@ int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream)
   if (out->h_last && a->bidirectional)
     return fail(RP_ERR_INVALID, "scan fwd: the final state exists for causal scans only");
   const Plan pl = make_plan(a);
-  if (out->ckpt && pl.ckpt_bytes > 0 && !aligned(out->ckpt, 4))
-    return fail(RP_ERR_INVALID, "scan fwd: misaligned checkpoint workspace");
+  if (out->ckpt && pl.ckpt_bytes > 0 && !aligned(out->ckpt, 256))
+    return fail(RP_ERR_INVALID, "scan fwd: checkpoint workspace must be 256-byte aligned");
   if (a->B == 0 || a->D == 0) return RP_OK;
   if (a->L == 0) {
     if (out->h_last) {
@@ -269,7 +279,11 @@ int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream)
   if ((int64_t)pl.ntiles * a->B > kI32Max)
     return fail(RP_ERR_UNSUPPORTED, "scan fwd: grid too large");
   const rp::ScanParams p = scan_params(a, pl);
-  rp::FwdOut o{out->y, pl.ckpt_bytes > 0 ? out->ckpt : nullptr, out->h_last, out->beta_last};
+  float* ck = pl.ckpt_bytes > 0 ? out->ckpt : nullptr;
+  float* dc = (ck != nullptr && pl.dcache_off >= 0)
+                  ? reinterpret_cast<float*>(reinterpret_cast<char*>(ck) + pl.dcache_off)
+                  : nullptr;
+  rp::FwdOut o{out->y, ck, out->h_last, out->beta_last, dc};
   hipError_t e = rp::launch_scan_fwd(pl.S, pl.NPL, pl.gk, p, o, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "scan fwd launch");
   return RP_OK;
@@ -285,8 +299,9 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
   if (work > 0) {
     if (!io->dy || !io->d_delta || !io->d_u)
       return fail(RP_ERR_INVALID, "scan bwd: NULL dy / d_delta / d_u");
-    if (pl.ckpt_bytes > 0 && !io->ckpt)
-      return fail(RP_ERR_INVALID, "scan bwd: checkpoint workspace required for L=%lld",
+    if (pl.ckpt_bytes > 0 && (!io->ckpt || !aligned(io->ckpt, 256)))
+      return fail(RP_ERR_INVALID,
+                  "scan bwd: 256-byte aligned checkpoint workspace required for L=%lld",
                   (long long)a->L);
   }
   if (a->B * a->L > 0 && (!io->d_Bc || !io->d_Cc))
@@ -313,6 +328,10 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
   rp::BwdIO b{};
   b.dy = io->dy;
   b.ckpt = io->ckpt;
+  b.dcache = pl.dcache_off >= 0
+                 ? reinterpret_cast<const float*>(reinterpret_cast<const char*>(io->ckpt) +
+                                                  pl.dcache_off)
+                 : nullptr;
   b.dh_last = io->dh_last;
   b.dbeta_last = io->dbeta_last;
   b.d_h0 = io->d_h0;
@@ -351,8 +370,9 @@ int rp_step_check(const rp_step_args* a) {
     return fail(RP_ERR_INVALID, "step args: NULL required pointer");
   if ((a->h_in == nullptr) != (a->beta_in == nullptr))
     return fail(RP_ERR_INVALID, "step args: h_in and beta_in go together");
-  if ((a->broadcast_state != 0 && a->broadcast_state != 1) || a->reserved != 0)
-    return fail(RP_ERR_INVALID, "step args: broadcast_state must be 0 or 1, reserved 0");
+  if ((a->broadcast_state != 0 && a->broadcast_state != 1) ||
+      (a->delta_softplus != 0 && a->delta_softplus != 1))
+    return fail(RP_ERR_INVALID, "step args: broadcast_state and delta_softplus must be 0 or 1");
   if (a->broadcast_state && a->h_in == nullptr)
     return fail(RP_ERR_INVALID, "step args: broadcast_state needs h_in / beta_in");
   if (a->broadcast_state) {
@@ -401,6 +421,7 @@ int rp_step(const rp_step_args* a, void* stream) {
   p.h_in = a->h_in;
   p.beta_in = a->beta_in;
   p.ssr = a->broadcast_state ? 0 : a->D * a->N;
+  p.dsp = a->delta_softplus;
   p.Ar = a->NR > 0 ? a->A_real : nullptr;
   p.Ai = a->NR > 0 ? a->A_imag : nullptr;
   p.Tk = a->NT > 0 ? a->track : nullptr;

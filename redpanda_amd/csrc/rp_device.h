@@ -71,6 +71,16 @@ __device__ __forceinline__ float load_in(const void* p, int64_t i, int dtype) {
 }
 
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }
+
+// delta = softplus(x) as torch computes it for the dt projection
+// (engine/mamba.py:300, F.softplus with beta 1, threshold 20, in fp32).
+__device__ __forceinline__ float softplus_of(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+// The same derivative from delta = softplus(x) itself: sigmoid(x) =
+// 1 - exp(-delta), as -expm1(-delta) (accurate for small delta; 1 above the
+// threshold, where delta = x > 20).
+__device__ __forceinline__ float softplus_grad_from_delta(float g, float delta) {
+  return fmul(g, -expm1f(-delta));
+}
 __device__ __forceinline__ float ffma(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
 // exp2 on the transcendental unit (v_exp_f32).

@@ -28,6 +28,7 @@ struct ScanParams {
   const float* beta0;
   int B, L, D, N, NR, NT;
   int dt_delta, dt_u, dt_B, dt_C;
+  int dsp;       // 1: delta holds x and the scan uses softplus(x)
   int ndir;      // 1 causal, 2 bidirectional
   int ntiles;    // ceil(D / CB)
   int nck;       // stored checkpoints per (dir, b): ceil(L / K) - 1
@@ -38,6 +39,7 @@ struct FwdOut {
   float* ckpt;
   float* h_last;
   float* beta_last;
+  float* dcache;  // (B, L, D) softplus(x) for the backward, or null
 };
 
 struct BwdIO {
@@ -49,6 +51,7 @@ struct BwdIO {
   float* d_u;
   float* d_h0;       // (B, D, N) or null
   float* d_beta0;
+  const float* dcache;  // (B, L, D) delta = softplus(x) cached by the forward (dsp only)
   float* part_bc;    // [2][ntiles][B][L][N]  per-tile dB / dC partial sums
   double* part_par;  // [nbg][2][D][N]        per-batch-group dA partial sums
   int bg;           // batch rows per workgroup
@@ -68,6 +71,7 @@ struct StepParams {
   const float* h_in;
   const float* beta_in;
   int64_t ssr;  // elements between consecutive rollouts' input states (0: one shared state)
+  int dsp;      // 1: delta holds x and the step uses softplus(x)
   const float* Ar;
   const float* Ai;
   const float* Tk;

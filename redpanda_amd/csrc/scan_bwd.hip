@@ -106,6 +106,13 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // slot (stage_store).  Steps and channels beyond the data load as zeros.
   uint32_t rdt[CPT], ru[CPT], rb[SPT], rc[SPT];
   float rdy[CPT];
+  // delta as staged: the input itself, or with softplus the forward's cache
+  // of softplus(x) (fp32, contiguous)
+  const bool cached = p.dsp != 0;
+  const void* dsrc = cached ? static_cast<const void*>(io.dcache) : p.delta;
+  const int64_t d_sb = cached ? (int64_t)L * p.D : p.dsb;
+  const int64_t d_sl = cached ? (int64_t)p.D : p.dsl;
+  const int d_dt = cached ? RP_F32 : p.dt_delta;
   auto stage_load = [&](int b, int dir, int ch) {
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
@@ -117,7 +124,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       rdy[k] = 0.f;
       if (e < KS * CB && i >= 0 && i < L && c2 < p.D) {
         const int t = tix(dir, i);
-        rdt[k] = load_raw(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
+        rdt[k] = load_raw(dsrc, (int64_t)b * d_sb + (int64_t)t * d_sl + c2, d_dt);
         ru[k] = load_raw(p.u, (int64_t)b * p.usb + (int64_t)t * p.usl + c2, p.dt_u);
         rdy[k] = io.dy[((int64_t)b * L + t) * p.D + c2];
       }
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     for (int k = 0; k < CPT; ++k) {
       const int e = tid + k * kThreads;
       if (e < KS * CB) {
-        const float dt = cvt_raw(rdt[k], p.dt_delta);
+        const float dt = cvt_raw(rdt[k], d_dt);
         const float uu = cvt_raw(ru[k], p.dt_u);
         sCh[SL][e / CB][e % CB] = make_float4(dt, 0.5f * fmul(dt, uu), 0.5f * uu, rdy[k]);
       }
@@ -195,6 +202,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     if (e >= K * CB || r >= kcnt || c2 >= p.D) return -1;
     return ((int64_t)b * L + tix(dir, i0 + r)) * p.D + c2;
   };
+  // whether this direction's d_delta store is the last one (the gradient
+  // is then complete and, with softplus, taken through it)
+  auto dd_final = [&](int dir) { return dir == p.ndir - 1; };
 
   const int b_lo = bgi * io.bg;
   const int b_hi = min(p.B, b_lo + io.bg);
@@ -403,7 +413,12 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   const int64_t idx = dd_index(e, b, dir, i0, kcnt);
                   if (idx >= 0) {
                     const float2 v = sDD[e / CB][e % CB];
-                    io.d_delta[idx] = dir == 0 ? v.x : pdd[k][0] + v.x;
+                    float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
+                    // with softplus, the complete gradient is taken through it
+                    // (delta of the element: row e / CB + 1 of the slot)
+                    if (p.dsp && dd_final(dir))
+                      dd = softplus_grad_from_delta(dd, sCh[SL][e / CB + 1][e % CB].x);
+                    io.d_delta[idx] = dd;
                     io.d_u[idx] = dir == 0 ? v.y : pdd[k][1] + v.y;
                   }
                 }

@@ -85,7 +85,14 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
         if (r < cnt && c2 < p.D) {
           const int i = i0 + r;
           const int t = dir ? (L - 1 - i) : i;
-          dt = load_in(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
+          const int64_t di = ((int64_t)b * L + t) * p.D + c2;
+          if (dir == 1 && o.dcache != nullptr) {
+            dt = o.dcache[di];  // cached by this workgroup's forward direction
+          } else {
+            dt = load_in(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
+            if (p.dsp) dt = softplus_of(dt);
+            if (o.dcache != nullptr) o.dcache[di] = dt;
+          }
           const float uu = load_in(p.u, (int64_t)b * p.usb + (int64_t)t * p.usl + c2, p.dt_u);
           hd = 0.5f * fmul(dt, uu);
         }

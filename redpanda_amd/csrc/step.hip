@@ -51,6 +51,7 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   float dt = 0.f, uu = 0.f;
   if (cvalid) {
     dt = p.delta[(int64_t)r * p.dsr + c];
+    if (p.dsp) dt = softplus_of(dt);
     uu = p.u[(int64_t)r * p.usr + c];
   }
   const int64_t sbase = ((int64_t)r * p.D + c) * p.N;  // output state
@@ -144,7 +145,8 @@ __device__ __forceinline__ void store_stream(float4* p, float4 v) {
 }
 
 // FULLD: D is a multiple of the workgroup's 256 channels (no channel guard).
-template <int S, int NPL, class GK, bool FULLD>
+// DSP: delta holds x and the step uses softplus(x).
+template <int S, int NPL, class GK, bool FULLD, bool DSP>
 __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
@@ -201,7 +203,8 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   for (int rr = 0; rr < nr; ++rr) {
     const int64_t r = r_lo + rr;
     const int64_t blk = (r * p.D + c0) * NV;  // float4 offset of the output block
-    const float dt = p.delta[r * p.dsr + cld];
+    float dt = p.delta[r * p.dsr + cld];
+    if constexpr (DSP) dt = softplus_of(dt);
     const float uu = p.u[r * p.usr + cld];
     if (p.h_in != nullptr) {
       // input block: the rollout's own, or the one shared state (ssr == 0)
@@ -280,14 +283,20 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   }
 }
 
-template <int S, int NPL, class GK>
-static hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
+template <int S, int NPL, class GK, bool DSP>
+static hipError_t launch_step_tile_d(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ctiles * p.rgroups));
   if (p.D % kStepTile == 0)
-    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP>), grid, dim3(kThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false, DSP>), grid, dim3(kThreads), 0, st, p);
   return hipGetLastError();
+}
+
+template <int S, int NPL, class GK>
+static hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
+  return p.dsp ? launch_step_tile_d<S, NPL, GK, true>(p, st)
+               : launch_step_tile_d<S, NPL, GK, false>(p, st);
 }
 
 template <int S, int NPL>

@@ -159,9 +159,11 @@ class Mamba3Block(nn.Module):
         return delta, B_raw.view(*lead, n, p), C_raw.view(*lead, n, p)
 
     def _ssm_proj_contracted(self, u):
-        """(delta, Bc, Cc): _ssm_proj followed by the sums over p
+        """(x_dt, Bc, Cc): _ssm_proj followed by the sums over p
         (engine/mamba.py:336-337), with BCNorm and the sums in one fused
-        kernel; Bc, Cc fp32 (..., d_state)."""
+        kernel; Bc, Cc fp32 (..., d_state).  x_dt is the dt projection
+        BEFORE softplus: the scan and step kernels apply softplus on load
+        (delta_softplus=True)."""
         cfg = self.config
         n, p = cfg.d_state, cfg.mimo_p
         dt_raw, B_raw, C_raw = self.x_proj(u).split([cfg.dt_rank, n * p, n * p], dim=-1)
@@ -170,8 +172,7 @@ class Mamba3Block(nn.Module):
                                      self.b_norm.eps)
         else:
             Bc, Cc = hip_bcnorm_psum(B_raw, C_raw, None, None, p, normalize=False)
-        delta = F.softplus(self.dt_proj(dt_raw))
-        return delta, Bc, Cc
+        return self.dt_proj(dt_raw), Bc, Cc
 
     # ── scan ──
 
@@ -190,18 +191,21 @@ class Mamba3Block(nn.Module):
         return y + u * D
 
     def _scan_core(self, u, delta, A_real, A_imag, B, C, return_state=False,
-                   bidirectional=False, contracted=False):
+                   bidirectional=False, contracted=False, delta_softplus=False):
         """The scan alone (no D-skip): y, or (y, (h_last, beta_last)).  B, C:
-        (..., n, p), or already contracted (..., n) with contracted=True."""
+        (..., n, p), or already contracted (..., n) with contracted=True;
+        delta_softplus: delta is the dt projection before softplus."""
         _need_device(u, "the selective scan")
         cfg = self.config
         Bc = B if contracted else B.sum(dim=-1)
         Cc = C if contracted else C.sum(dim=-1)
         track = self._track_or_none()
         if return_state:
-            return hip_scan_with_state(delta, u, Bc, Cc, A_real, A_imag, track)
+            return hip_scan_with_state(delta, u, Bc, Cc, A_real, A_imag, track,
+                                       delta_softplus=delta_softplus)
         return hip_trapezoidal_scan(delta, u, Bc, Cc, A_real, A_imag, track,
-                                    cfg.n_rot_state, cfg.d_state, bidirectional=bidirectional)
+                                    cfg.n_rot_state, cfg.d_state, bidirectional=bidirectional,
+                                    delta_softplus=delta_softplus)
 
     def ssm(self, u, return_state=False):
         delta, B, C = self._ssm_proj(u)
@@ -214,21 +218,21 @@ class Mamba3Block(nn.Module):
         and the D-skip and silu(z) gate one fused pass after it."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        delta, Bc, Cc = self._ssm_proj_contracted(x_branch)
+        x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
         bi = self.config.bidirectional
-        y = self._scan_core(x_branch, delta, A_real, A_imag, Bc, Cc, bidirectional=bi,
-                            contracted=True)
+        y = self._scan_core(x_branch, x_dt, A_real, A_imag, Bc, Cc, bidirectional=bi,
+                            contracted=True, delta_softplus=True)
         return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 2 if bi else 1))
 
     def forward_with_state(self, x):
         """engine/mamba.py:269-282: output plus the final (h, beta) cache."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        delta, Bc, Cc = self._ssm_proj_contracted(x_branch)
+        x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
-        y, state = self._scan_core(x_branch, delta, A_real, A_imag, Bc, Cc, return_state=True,
-                                   contracted=True)
+        y, state = self._scan_core(x_branch, x_dt, A_real, A_imag, Bc, Cc, return_state=True,
+                                   contracted=True, delta_softplus=True)
         return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1)), state
 
     # ── O(1) step (engine/mamba.py:427-498) ──
@@ -240,7 +244,7 @@ class Mamba3Block(nn.Module):
         cfg = self.config
         x_branch, z = self.in_proj(x_t).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        delta, Bc, Cc = self._ssm_proj_contracted(x_branch)
+        x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
         track = self._track_or_none()
         grad = torch.is_grad_enabled() and (
@@ -248,13 +252,14 @@ class Mamba3Block(nn.Module):
             (state is not None and any(s.requires_grad for s in state)))
         if grad:
             # differentiable: a length-1 scan from the cached state
-            y, (h, beta) = hip_scan_with_state(delta.unsqueeze(1), x_branch.unsqueeze(1),
+            y, (h, beta) = hip_scan_with_state(x_dt.unsqueeze(1), x_branch.unsqueeze(1),
                                                Bc.unsqueeze(1), Cc.unsqueeze(1),
-                                               A_real, A_imag, track, state=state)
+                                               A_real, A_imag, track, state=state,
+                                               delta_softplus=True)
             y = y.squeeze(1) + x_branch * self.D
         else:
-            y, (h, beta) = hip_step(delta, x_branch, Bc, Cc, A_real, A_imag, track, self.D,
-                                    state)
+            y, (h, beta) = hip_step(x_dt, x_branch, Bc, Cc, A_real, A_imag, track, self.D,
+                                    state, delta_softplus=True)
         out = self.out_proj(y * F.silu(z))
         return out, (h, beta)
 

@@ -38,9 +38,11 @@ def _code(t):
         raise TypeError(f"redpanda_amd scan: unsupported dtype {t.dtype}") from None
 
 
-def make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional, h0=None, beta0=None):
+def make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional, h0=None, beta0=None,
+                   delta_softplus=False):
     """ScanArgs for device tensors (delta/u (B,L,D), Bc/Cc (B,L,N); optional
-    (B,D,N) fp32 contiguous initial state h0, beta0)."""
+    (B,D,N) fp32 contiguous initial state h0, beta0).  delta_softplus: delta
+    holds the dt projection x and the kernels use softplus(x)."""
     B, L, D = u.shape
     N = Bc.shape[-1]
     NR = 0 if Ar is None else Ar.shape[-1]
@@ -49,7 +51,7 @@ def make_scan_args(delta, u, Bc, Cc, Ar, Ai, Tk, bidirectional, h0=None, beta0=N
     a.B, a.L, a.D, a.N, a.NR, a.NT = B, L, D, N, NR, NT
     a.dtype_delta, a.dtype_u, a.dtype_B, a.dtype_C = _code(delta), _code(u), _code(Bc), _code(Cc)
     a.bidirectional = 1 if bidirectional else 0
-    a.reserved = 0
+    a.delta_softplus = 1 if delta_softplus else 0
     a.delta, a.delta_sb, a.delta_sl = delta.data_ptr(), delta.stride(0), delta.stride(1)
     a.u, a.u_sb, a.u_sl = u.data_ptr(), u.stride(0), u.stride(1)
     a.Bc, a.Bc_sb, a.Bc_sl = Bc.data_ptr(), Bc.stride(0), Bc.stride(1)
@@ -88,7 +90,8 @@ class _HipScan(torch.autograd.Function):
     (h0, beta0) and optionally returning the final state (h_last, beta_last)."""
 
     @staticmethod
-    def forward(ctx, delta, u, Bc, Cc, Ar, Ai, Tk, h0, beta0, bidirectional, with_state):
+    def forward(ctx, delta, u, Bc, Cc, Ar, Ai, Tk, h0, beta0, bidirectional, with_state,
+                delta_softplus=False):
         lib = _lib.load()
         delta, u, Bc, Cc = (_inner_contig(t) for t in (delta, u, Bc, Cc))
         Arc, Aic, Tkc = _param(Ar), _param(Ai), _param(Tk)
@@ -96,7 +99,8 @@ class _HipScan(torch.autograd.Function):
         B, L, D = u.shape
         N = Bc.shape[-1]
         dev = u.device
-        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, bidirectional, h0c, b0c)
+        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, bidirectional, h0c, b0c,
+                              delta_softplus)
         y = torch.empty((B, L, D), dtype=torch.float32, device=dev)
         need_grad = any(ctx.needs_input_grad[:9])
         ckpt = None
@@ -112,6 +116,7 @@ class _HipScan(torch.autograd.Function):
         _lib.check(lib.rp_scan_fwd(ctypes.byref(args), ctypes.byref(out), _lib.stream_of(dev)), lib)
         ctx.bidirectional = bidirectional
         ctx.with_state = with_state
+        ctx.delta_softplus = delta_softplus
         ctx.in_dtypes = tuple(None if t is None else t.dtype
                               for t in (delta, u, Bc, Cc, Ar, Ai, Tk, h0, beta0))
         if need_grad:
@@ -127,7 +132,8 @@ class _HipScan(torch.autograd.Function):
         B, L, D = u.shape
         N = Bc.shape[-1]
         dev = u.device
-        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, ctx.bidirectional, h0c, b0c)
+        args = make_scan_args(delta, u, Bc, Cc, Arc, Aic, Tkc, ctx.bidirectional, h0c, b0c,
+                              ctx.delta_softplus)
         f32 = dict(dtype=torch.float32, device=dev)
         dy = torch.zeros((B, L, D), **f32) if dy is None else dy.to(torch.float32).contiguous()
         if dh_last is not None:
@@ -157,17 +163,19 @@ class _HipScan(torch.autograd.Function):
         out = []
         for g, dt, need in zip(grads, ctx.in_dtypes, ctx.needs_input_grad[:9]):
             out.append(g.to(dt) if (g is not None and need) else None)
-        return (*out, None, None)
+        return (*out, None, None, None)
 
 
 def hip_trapezoidal_scan(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
-                         n_rot, n_state, bidirectional=False):
+                         n_rot, n_state, bidirectional=False, delta_softplus=False):
     """Drop-in for the reference's triton_trapezoidal_scan (engine/triton_scan.py:318-337).
 
     delta, u: (B, L, D); B_contracted, C_contracted: (B, L, N); A_real,
     A_imag: (D, n_rot) or None; track: (D, n_state - n_rot) tanh gates or
     None.  Returns y (B, L, D) fp32 without the u*D skip.  With
     bidirectional=True returns S(x) + flip(S(flip(x))) from one fused launch.
+    With delta_softplus=True, `delta` is the dt projection x and the scan runs
+    on F.softplus(x) (engine/mamba.py:300), differentiable in x.
     """
     if A_real is not None and A_real.shape[-1] != n_rot:
         raise ValueError(f"scan: A_real has {A_real.shape[-1]} states, n_rot={n_rot}")
@@ -179,11 +187,11 @@ def hip_trapezoidal_scan(delta, u, B_contracted, C_contracted, A_real, A_imag, t
     if B_contracted.shape[-1] != n_state:
         raise ValueError(f"scan: B_contracted has {B_contracted.shape[-1]} states, n_state={n_state}")
     return _HipScan.apply(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
-                          None, None, bool(bidirectional), False)
+                          None, None, bool(bidirectional), False, bool(delta_softplus))
 
 
 def hip_scan_with_state(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
-                        state=None):
+                        state=None, delta_softplus=False):
     """Causal scan continuing from `state` = (h0, beta0) (or the zero state)
     and returning (y, (h_last, beta_last)): the return_state path of the
     reference (engine/mamba.py:377-379) on the HIP kernel.  Differentiable in
@@ -200,7 +208,7 @@ def hip_scan_with_state(delta, u, B_contracted, C_contracted, A_real, A_imag, tr
         if L < 1:
             raise ValueError("scan: an initial state needs L >= 1")
     y, h, beta = _HipScan.apply(delta, u, B_contracted, C_contracted, A_real, A_imag, track,
-                                h0, beta0, False, True)
+                                h0, beta0, False, True, bool(delta_softplus))
     return y, (h, beta)
 
 

@@ -41,13 +41,16 @@ def _state_pair(h, b, R, D, N):
     return h.contiguous(), b.contiguous(), 0
 
 
-def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None):
+def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None,
+             delta_softplus=False):
     """One step for R rollouts.
 
     delta, u: (R, D); Bc, Cc: (R, N) (contracted over p); A_real/A_imag:
     (D, NR) or None; track: (D, NT) or None; Dskip: (D,); state: (h, beta)
     fp32 (R, D, N) (or an expansion of one (1, D, N) state) or None for a
-    fresh state.  Returns (y (R, D) incl. u*D, (h_new, beta_new)).
+    fresh state.  Returns (y (R, D) incl. u*D, (h_new, beta_new)).  With
+    delta_softplus, `delta` is the dt projection x and the step uses
+    F.softplus(x) (engine/mamba.py:300).
     """
     lib = _lib.load()
     R, D = u.shape
@@ -85,5 +88,6 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     a.Dskip = Dk.data_ptr()
     a.h_out, a.beta_out, a.y = h_out.data_ptr(), beta_out.data_ptr(), y.data_ptr()
     a.broadcast_state = broadcast
+    a.delta_softplus = 1 if delta_softplus else 0
     _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
     return y, (h_out, beta_out)

@@ -67,7 +67,7 @@ def test_valid_args_pass_check(lib):
     ("delta", None, "NULL"),
     ("track", None, "track"),
     ("u_sl", -5, "stride"),
-    ("reserved", 1, "reserved"),
+    ("delta_softplus", 2, "delta_softplus"),
 ])
 def test_invalid_scan_args_rejected(lib, field, value, needle):
     kw = {field: value}
@@ -139,7 +139,8 @@ def test_step_broadcast_state_rules(lib):
               beta_out=0x400000)
     assert lib.rp_step_check(ctypes.byref(_step_args(**ok))) == 0
     assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "broadcast_state": 2}))) < 0
-    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "reserved": 1}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "delta_softplus": 2}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "delta_softplus": 1}))) == 0
     assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "h_in": None,
                                                          "beta_in": None}))) < 0
     # in place would let one rollout overwrite the state the others still read
