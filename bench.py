@@ -125,6 +125,13 @@ def step_bytes(R, D, N, NR, NT):
     return R * (16 * D * N + 12 * D + 8 * N) + (2 * D * NR + D * NT + D) * 4
 
 
+def step_bytes_rank1(R, D, N, NR, NT):
+    """The same with beta in rank-1 rows [dt*u | B]: read and write h (8 B
+    per state element) and the D + N floats of the row (8 B each), plus the
+    per-channel and per-state inputs and y as above."""
+    return R * (8 * D * N + 8 * (D + N) + 12 * D + 8 * N) + (2 * D * NR + D * NT + D) * 4
+
+
 class EventTimer:
     """Average GPU duration of a launch sequence, with events on the stream
     the kernels are launched on (torch's current stream)."""
@@ -305,9 +312,42 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
     ab.h_in, ab.beta_in, ab.broadcast_state = shared_h.data_ptr(), shared_b.data_ptr(), 1
     t_shared = timer.time(lambda: _lib.check(lib.rp_step(ctypes.byref(ab), stream), lib), 10)
     nb_shared = R * (8 * D * N + 12 * D + 8 * N) + 8 * D * N + (2 * D * NR + D * NT + D) * 4
+    # the same plies with the cache's beta in rank-1 rows (R, D + N): the
+    # rows ping-pong between two buffers (a rank-1 step may not update them
+    # in place); h is updated in place as above
+    compact = []
+    for a, keep_t in per_layer:
+        bp = [torch.zeros((R, D + N), **f32), torch.zeros((R, D + N), **f32)]
+        pair = []
+        for i in range(2):
+            ar = _lib.StepArgs.from_buffer_copy(a)
+            ar.beta_rank1 = 1
+            ar.beta_in, ar.beta_out = bp[i].data_ptr(), bp[1 - i].data_ptr()
+            pair.append(ar)
+        compact.append((pair, bp, keep_t))
+    parity = [0]
+
+    def ply_compact():
+        i = parity[0]
+        for pair, _, _ in compact:
+            _lib.check(lib.rp_step(ctypes.byref(pair[i]), stream), lib)
+        parity[0] = 1 - i
+
+    for _ in range(max(args.warmup, 1)):
+        ply_compact()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(plies):
+        ply_compact()
+    torch.cuda.synchronize()
+    elapsed_c = time.perf_counter() - t0
+    t_launch_c = timer.time(ply_compact, plies) / layers
+    nb_c = step_bytes_rank1(R, D, N, NR, NT)
     return dict(rollout_steps_s=R * plies / elapsed, plies=plies, elapsed=elapsed,
                 t_launch=t_launch, bytes=nb, GBps=nb / t_launch / 1e9,
-                t_shared=t_shared, bytes_shared=nb_shared, GBps_shared=nb_shared / t_shared / 1e9)
+                t_shared=t_shared, bytes_shared=nb_shared, GBps_shared=nb_shared / t_shared / 1e9,
+                rollout_steps_s_rank1=R * plies / elapsed_c, t_launch_rank1=t_launch_c,
+                bytes_rank1=nb_c, GBps_rank1=nb_c / t_launch_c / 1e9)
 
 
 def mixer_inputs(torch, dev, seed):
@@ -730,7 +770,9 @@ def main():
         print(f"[bench] step {STEP_SHAPE}", file=sys.stderr, flush=True)
         step = bench_step(torch, args)
         print(f"[bench] step: {step['rollout_steps_s']:.4g} rollout-steps/s, "
-              f"{step['t_launch'] * 1e6:.1f} us/launch, {step['GBps']:.0f} GB/s",
+              f"{step['t_launch'] * 1e6:.1f} us/launch, {step['GBps']:.0f} GB/s; rank-1 cache "
+              f"{step['rollout_steps_s_rank1']:.4g} rollout-steps/s, "
+              f"{step['t_launch_rank1'] * 1e6:.1f} us/launch, {step['GBps_rank1']:.0f} GB/s",
               file=sys.stderr, flush=True)
     lng = None
     if not args.no_long:
@@ -801,6 +843,14 @@ def main():
                          "alg_bytes_per_launch": step["bytes"],
                          "avg_launch_s": step["t_launch"]},
             "cpu_baseline": step.get("cpu_baseline"),
+            "rank1_cache": {
+                "workload": "the same plies with each layer's beta cached as rank-1 rows "
+                            "[dt*u | B] (D + N floats per rollout; bit-identical results)",
+                "value": step["rollout_steps_s_rank1"], "unit": "rollout-steps/s",
+                "avg_launch_s": step["t_launch_rank1"],
+                "alg_bytes_per_launch": step["bytes_rank1"],
+                "achieved_GBps": step["GBps_rank1"],
+                "frac": step["GBps_rank1"] / HBM_PEAK_GBS},
             "from_shared_state": {
                 "workload": "first ply after a batch-1 cache is fanned out to the rollouts "
                             "(broadcast input state, no copies)",

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 5
+#define RP_ABI_VERSION 6
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -133,6 +133,12 @@ typedef struct rp_scan_bwd_io {
  * rollout continues from -- a batch-1 cache fanned out to R rollouts without
  * the copies of engine/search_mamba.py:177-187 (expand().contiguous()); the
  * outputs must then not overlap the inputs.  0: the (R, D, N) layout above.
+ * beta_rank1 = 1: beta is carried by its rank-1 factors, since beta =
+ * (dt u) outer B: beta_in / beta_out are (R, D + N) fp32 rows [dt*u | B]
+ * (one (D + N) row with broadcast_state), and the step forms beta_prev =
+ * (dt*u)_prev * B_prev with the multiply that produced the full form, so the
+ * results are the same bits at half the state traffic.  beta_out must not
+ * overlap beta_in (a rollout's B row is read by all its channel tiles).
  */
 typedef struct rp_step_args {
   int64_t R, D, N, NR, NT;
@@ -151,6 +157,8 @@ typedef struct rp_step_args {
   float* y;
   int32_t broadcast_state;  /* 0 or 1, see above */
   int32_t delta_softplus;   /* 0 or 1: delta holds x, the step uses softplus(x) */
+  int32_t beta_rank1;       /* 0 or 1, see above */
+  int32_t reserved;         /* must be 0 */
 } rp_step_args;
 
 /*

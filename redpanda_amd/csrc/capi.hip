@@ -371,19 +371,30 @@ int rp_step_check(const rp_step_args* a) {
   if ((a->h_in == nullptr) != (a->beta_in == nullptr))
     return fail(RP_ERR_INVALID, "step args: h_in and beta_in go together");
   if ((a->broadcast_state != 0 && a->broadcast_state != 1) ||
-      (a->delta_softplus != 0 && a->delta_softplus != 1))
-    return fail(RP_ERR_INVALID, "step args: broadcast_state and delta_softplus must be 0 or 1");
+      (a->delta_softplus != 0 && a->delta_softplus != 1) ||
+      (a->beta_rank1 != 0 && a->beta_rank1 != 1) || a->reserved != 0)
+    return fail(RP_ERR_INVALID,
+                "step args: broadcast_state, delta_softplus and beta_rank1 must be 0 or 1, "
+                "reserved 0");
   if (a->broadcast_state && a->h_in == nullptr)
     return fail(RP_ERR_INVALID, "step args: broadcast_state needs h_in / beta_in");
-  if (a->broadcast_state) {
-    // every rollout reads the one input state while others write theirs
-    const int64_t in_bytes = a->D * a->N * 4, out_bytes = a->R * a->D * a->N * 4;
-    const float* ins[] = {a->h_in, a->beta_in};
-    const float* outs[] = {a->h_out, a->beta_out};
-    for (const float* i : ins)
-      for (const float* o : outs)
-        if (overlaps(i, in_bytes, o, out_bytes))
-          return fail(RP_ERR_INVALID, "step args: a broadcast input state overlaps an output");
+  {
+    // bytes of the input and output h and beta blocks
+    const int64_t rows_in = a->broadcast_state ? 1 : a->R;
+    const int64_t h_in_b = rows_in * a->D * a->N * 4, h_out_b = a->R * a->D * a->N * 4;
+    const int64_t bw = a->beta_rank1 ? a->D + a->N : a->D * a->N;
+    const int64_t b_in_b = rows_in * bw * 4, b_out_b = a->R * bw * 4;
+    if (a->broadcast_state) {
+      // every rollout reads the one input state while others write theirs
+      if (overlaps(a->h_in, h_in_b, a->h_out, h_out_b) ||
+          overlaps(a->h_in, h_in_b, a->beta_out, b_out_b) ||
+          overlaps(a->beta_in, b_in_b, a->h_out, h_out_b) ||
+          overlaps(a->beta_in, b_in_b, a->beta_out, b_out_b))
+        return fail(RP_ERR_INVALID, "step args: a broadcast input state overlaps an output");
+    }
+    // a rank-1 row's B part is read by every channel tile of the rollout
+    if (a->beta_rank1 && a->h_in && overlaps(a->beta_in, b_in_b, a->beta_out, b_out_b))
+      return fail(RP_ERR_INVALID, "step args: rank-1 beta_out must not overlap beta_in");
   }
   if (a->NR > 0 && !a->A_real) return fail(RP_ERR_INVALID, "step args: NR>0 needs A_real");
   if (a->NR == 0 && a->A_imag) return fail(RP_ERR_INVALID, "step args: A_imag without NR");
@@ -422,6 +433,8 @@ int rp_step(const rp_step_args* a, void* stream) {
   p.beta_in = a->beta_in;
   p.ssr = a->broadcast_state ? 0 : a->D * a->N;
   p.dsp = a->delta_softplus;
+  p.rank1 = a->beta_rank1;
+  p.bssr = a->broadcast_state ? 0 : a->D + a->N;
   p.Ar = a->NR > 0 ? a->A_real : nullptr;
   p.Ai = a->NR > 0 ? a->A_imag : nullptr;
   p.Tk = a->NT > 0 ? a->track : nullptr;
@@ -435,8 +448,9 @@ int rp_step(const rp_step_args* a, void* stream) {
   const int gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
   // the tile kernel moves each channel's (h, beta) as 16-byte vectors
   const bool tile = a->N % 4 == 0 && S * NPL == a->N && a->N <= 40 && aligned(a->h_out, 16) &&
-                    aligned(a->beta_out, 16) &&
-                    (a->h_in == nullptr || (aligned(a->h_in, 16) && aligned(a->beta_in, 16)));
+                    (a->h_in == nullptr || aligned(a->h_in, 16)) &&
+                    (a->beta_rank1 || (aligned(a->beta_out, 16) &&
+                                       (a->h_in == nullptr || aligned(a->beta_in, 16))));
   if (tile) {
     p.ctiles = (int)((a->D + rp::kStepTile - 1) / rp::kStepTile);
     // rollouts per workgroup: a few amortise the workgroup's prologue (gate

@@ -72,6 +72,8 @@ struct StepParams {
   const float* beta_in;
   int64_t ssr;  // elements between consecutive rollouts' input states (0: one shared state)
   int dsp;      // 1: delta holds x and the step uses softplus(x)
+  int rank1;    // 1: beta as rows [dt*u | B] of D + N floats
+  int64_t bssr; // rank-1 input rows: elements between rollouts (0: one shared row)
   const float* Ar;
   const float* Ai;
   const float* Tk;

@@ -69,7 +69,10 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
     }
     if (cvalid && n < p.N && p.h_in != nullptr) {
       h[j] = p.h_in[ibase + n];
-      hbp[j] = 0.5f * p.beta_in[ibase + n];
+      // beta_prev / 2: full form, or rank-1 (dt*u)_prev / 2 * B_prev
+      hbp[j] = p.rank1 ? fmul(0.5f * p.beta_in[(int64_t)r * p.bssr + c],
+                              p.beta_in[(int64_t)r * p.bssr + p.D + n])
+                       : 0.5f * p.beta_in[ibase + n];
     }
   }
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
@@ -83,11 +86,17 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
       const int n = j * S + s;
       if (n < p.N) {
         p.h_out[sbase + n] = h[j];
-        p.beta_out[sbase + n] = 2.f * hbp[j];
+        if (!p.rank1) p.beta_out[sbase + n] = 2.f * hbp[j];
       }
     }
-    if (s == 0) p.y[(int64_t)r * p.D + c] = y + fmul(uu, p.Dskip[c]);
+    if (s == 0) {
+      p.y[(int64_t)r * p.D + c] = y + fmul(uu, p.Dskip[c]);
+      if (p.rank1) p.beta_out[(int64_t)r * (p.D + p.N) + c] = fmul(dt, uu);
+    }
   }
+  // rank-1: the rollout's B row, written once (by its first channel tile)
+  if (p.rank1 && tile == 0 && tid < p.N)
+    p.beta_out[(int64_t)r * (p.D + p.N) + p.D + tid] = p.Bc[(int64_t)r * p.bsr + tid];
 }
 
 template <int S, int NPL, class GK>
@@ -146,13 +155,16 @@ __device__ __forceinline__ void store_stream(float4* p, float4 v) {
 
 // FULLD: D is a multiple of the workgroup's 256 channels (no channel guard).
 // DSP: delta holds x and the step uses softplus(x).
-template <int S, int NPL, class GK, bool FULLD, bool DSP>
+// RANK1: beta travels as rows [dt*u | B] (D + N floats per rollout); only
+// h moves through the LDS block, and beta_prev = (dt*u)_prev * B_prev.
+template <int S, int NPL, class GK, bool FULLD, bool DSP, bool RANK1>
 __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
   constexpr int TCH = kStepTile;
+  constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
   __shared__ float2 sTab[kTab];           // cos, sin of 2 pi k / kTab
-  __shared__ float sBC[kStepRiMax][2 * NP];  // B, C rows of the workgroup's rollouts
+  __shared__ float sBC[kStepRiMax][NBC * NP];  // B, C (B_prev) rows of the workgroup's rollouts
   // the (h, beta) block of one rollout: TCH channels x NP states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NV
   __shared__ float4 sH[TCH * NV], sBt[TCH * NV];
@@ -170,15 +182,22 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   // The prologue issues every load (B / C rows, gate parameters, D) before
   // it stores anything, so their latencies overlap.  The B / C rows of all
   // the workgroup's rollouts are staged once.
-  constexpr int BCPT = (kStepRiMax * 2 * NP + kThreads - 1) / kThreads;
+  constexpr int BCPT = (kStepRiMax * NBC * NP + kThreads - 1) / kThreads;
   float bc[BCPT];
 #pragma unroll
   for (int k = 0; k < BCPT; ++k) {
     const int e = tid + k * kThreads;
-    const int rr = e / (2 * NP), q = e % (2 * NP);
+    const int rr = e / (NBC * NP), q = e % (NBC * NP);
     const int64_t r = r_lo + rr;
     bc[k] = 0.f;
-    if (e < nr * 2 * NP) bc[k] = q < NP ? p.Bc[r * p.bsr + q] : p.Cc[r * p.csr + (q - NP)];
+    if (e < nr * NBC * NP) {
+      if (q < NP)
+        bc[k] = p.Bc[r * p.bsr + q];
+      else if (q < 2 * NP)
+        bc[k] = p.Cc[r * p.csr + (q - NP)];
+      else if (p.beta_in != nullptr)  // B_prev: the tail of the rank-1 row
+        bc[k] = p.beta_in[r * p.bssr + p.D + (q - 2 * NP)];
+    }
   }
   // the channel's gate parameters stay in registers for all its rollouts
   GateRaw graw[NP];
@@ -189,7 +208,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
   for (int k = 0; k < BCPT; ++k) {
     const int e = tid + k * kThreads;
-    if (e < nr * 2 * NP) sBC[e / (2 * NP)][e % (2 * NP)] = bc[k];
+    if (e < nr * NBC * NP) sBC[e / (NBC * NP)][e % (NBC * NP)] = bc[k];
   }
   float pah[NP], wh[NP];
 #pragma unroll
@@ -206,7 +225,10 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     float dt = p.delta[r * p.dsr + cld];
     if constexpr (DSP) dt = softplus_of(dt);
     const float uu = p.u[r * p.usr + cld];
+    // rank-1: the channel's (dt*u)_prev, halved as the scan halves dt*u
+    float hdp = 0.f;
     if (p.h_in != nullptr) {
+      if constexpr (RANK1) hdp = 0.5f * p.beta_in[r * p.bssr + cld];
       // input block: the rollout's own, or the one shared state (ssr == 0)
       const int64_t iblk = r * (p.ssr / 4) + (int64_t)c0 * NV;
       const float4* hi4 = reinterpret_cast<const float4*>(p.h_in) + iblk;
@@ -217,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
         const int k = tid + m * TCH;
         if (FULLD || k < nvalid) {
           hl[m] = load_stream(hi4 + k);
-          bl[m] = load_stream(bi4 + k);
+          if constexpr (!RANK1) bl[m] = load_stream(bi4 + k);
         }
       }
 #pragma unroll
@@ -225,14 +247,14 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
         const int k = tid + m * TCH;
         if (FULLD || k < nvalid) {
           sH[k] = hl[m];
-          sBt[k] = bl[m];
+          if constexpr (!RANK1) sBt[k] = bl[m];
         }
       }
     } else {
 #pragma unroll
       for (int m = 0; m < NV; ++m) {
         sH[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
-        sBt[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (!RANK1) sBt[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
     __syncthreads();  // the block (and, the first time, the table and B / C rows)
@@ -240,10 +262,11 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       h4[v] = sH[tid * NV + v];
-      b4[v] = sBt[tid * NV + v];
+      if constexpr (!RANK1) b4[v] = sBt[tid * NV + v];
     }
     const float* Bs = sBC[rr];
     const float* Cs = sBC[rr] + NP;
+    const float* Bp = sBC[rr] + (NBC - 1) * NP;  // B_prev (rank-1 only)
     const float hd = 0.5f * fmul(dt, uu);
     float ys[S];
 #pragma unroll
@@ -253,20 +276,28 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       const int j = n / S, q = n % S;
       float& hs = (&h4[n / 4].x)[n % 4];
       float& bs = (&b4[n / 4].x)[n % 4];
-      const float hbp = 0.5f * bs;
+      // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
+      // same bits as the product the full form stored
+      const float hbp = RANK1 ? fmul(hdp, Bp[n]) : 0.5f * bs;
       float unused;
       const float g = gate_of<S, GK, false>(j, q, p.NR, has_imag, dt, pah[n], wh[n], sTab, unused);
       const float hb = fmul(hd, Bs[n]);
       const float sm = hs + hbp;
       hs = ffma(g, sm, hb);
-      bs = 2.f * hb;
+      if constexpr (!RANK1) bs = 2.f * hb;
       ys[q] = ffma(hs, Cs[n], ys[q]);
     }
-    if (cvalid) p.y[r * p.D + c] = tree_sum<S>(ys) + fmul(uu, dsk);
+    if (cvalid) {
+      p.y[r * p.D + c] = tree_sum<S>(ys) + fmul(uu, dsk);
+      if constexpr (RANK1) p.beta_out[r * (p.D + N) + c] = fmul(dt, uu);
+    }
+    if constexpr (RANK1) {
+      if (tile == 0 && tid < N) p.beta_out[r * (p.D + N) + p.D + tid] = Bs[tid];
+    }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       sH[tid * NV + v] = h4[v];
-      sBt[tid * NV + v] = b4[v];
+      if constexpr (!RANK1) sBt[tid * NV + v] = b4[v];
     }
     __syncthreads();  // the updated block
     float4* ho4 = reinterpret_cast<float4*>(p.h_out) + blk;
@@ -276,27 +307,32 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       const int k = tid + m * TCH;
       if (FULLD || k < nvalid) {
         store_stream(ho4 + k, sH[k]);
-        store_stream(bo4 + k, sBt[k]);
+        if constexpr (!RANK1) store_stream(bo4 + k, sBt[k]);
       }
     }
     __syncthreads();  // the block's LDS is free for the next rollout
   }
 }
 
-template <int S, int NPL, class GK, bool DSP>
+template <int S, int NPL, class GK, bool DSP, bool RANK1>
 static hipError_t launch_step_tile_d(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ctiles * p.rgroups));
   if (p.D % kStepTile == 0)
-    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1>), grid, dim3(kThreads), 0,
+                       st, p);
   else
-    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false, DSP>), grid, dim3(kThreads), 0, st, p);
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false, DSP, RANK1>), grid, dim3(kThreads), 0,
+                       st, p);
   return hipGetLastError();
 }
 
 template <int S, int NPL, class GK>
 static hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
-  return p.dsp ? launch_step_tile_d<S, NPL, GK, true>(p, st)
-               : launch_step_tile_d<S, NPL, GK, false>(p, st);
+  if (p.rank1)
+    return p.dsp ? launch_step_tile_d<S, NPL, GK, true, true>(p, st)
+                 : launch_step_tile_d<S, NPL, GK, false, true>(p, st);
+  return p.dsp ? launch_step_tile_d<S, NPL, GK, true, false>(p, st)
+               : launch_step_tile_d<S, NPL, GK, false, false>(p, st);
 }
 
 template <int S, int NPL>

@@ -36,7 +36,7 @@ import torch.utils.checkpoint
 from redpanda_amd.bcnorm import hip_bcnorm_psum
 from redpanda_amd.mixer import hip_mixer_out
 from redpanda_amd.scan import hip_scan_with_state, hip_trapezoidal_scan
-from redpanda_amd.step import hip_step
+from redpanda_amd.step import compact_beta, full_beta, hip_step, is_compact
 
 # Chunk length of the reference's streaming scan (engine/mamba.py:101); kept
 # as a module constant for callers that read it.  The HIP scan is not chunked.
@@ -225,21 +225,36 @@ class Mamba3Block(nn.Module):
                             contracted=True, delta_softplus=True)
         return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 2 if bi else 1))
 
-    def forward_with_state(self, x):
-        """engine/mamba.py:269-282: output plus the final (h, beta) cache."""
+    def forward_with_state(self, x, compact=False):
+        """engine/mamba.py:269-282: output plus the final (h, beta) cache.
+        compact=True returns beta as its rank-1 row [dt*u | B] of the last
+        token (B, d_inner + d_state), which step() continues from with the
+        same results at half the state traffic."""
         x_branch, z = self.in_proj(x).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
         x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
         A_real, A_imag = self._compute_A()
-        y, state = self._scan_core(x_branch, x_dt, A_real, A_imag, Bc, Cc, return_state=True,
-                                   contracted=True, delta_softplus=True)
-        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1)), state
+        y, (h, beta) = self._scan_core(x_branch, x_dt, A_real, A_imag, Bc, Cc, return_state=True,
+                                       contracted=True, delta_softplus=True)
+        if compact:
+            beta = self._compact_beta(x_dt[:, -1], x_branch[:, -1], Bc[:, -1])
+        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1)), (h, beta)
+
+    @staticmethod
+    def _compact_beta(x_dt, u, Bc):
+        """Rank-1 row [dt*u | B] of one token's beta, dt = softplus(x_dt) in
+        fp32 as the kernels compute it (differentiable torch ops)."""
+        dtu = F.softplus(x_dt.float()) * u.float()
+        return compact_beta(dtu, Bc)
 
     # ── O(1) step (engine/mamba.py:427-498) ──
 
-    def step(self, x_t, state=None):
+    def step(self, x_t, state=None, compact=False):
         """One token for a batch: x_t (B, d_model), state (h, beta) fp32
-        (B, d_inner, d_state) or None.  Returns (out (B, d_model), (h, beta))."""
+        (B, d_inner, d_state) or None.  Returns (out (B, d_model), (h, beta)).
+        beta may also be in rank-1 rows (B, d_inner + d_state) (see
+        forward_with_state); the new state keeps the form of the one given,
+        or with no state the form `compact` asks for."""
         _need_device(x_t, "step()")
         cfg = self.config
         x_branch, z = self.in_proj(x_t).chunk(2, dim=-1)
@@ -250,16 +265,22 @@ class Mamba3Block(nn.Module):
         grad = torch.is_grad_enabled() and (
             any(p.requires_grad for p in self.parameters()) or x_t.requires_grad or
             (state is not None and any(s.requires_grad for s in state)))
+        rank1 = is_compact(state[1]) if state is not None else bool(compact)
         if grad:
-            # differentiable: a length-1 scan from the cached state
+            # differentiable: a length-1 scan from the cached state (a rank-1
+            # beta expanded to its full form first)
+            if state is not None and rank1:
+                state = (state[0], full_beta(state[1], cfg.d_inner))
             y, (h, beta) = hip_scan_with_state(x_dt.unsqueeze(1), x_branch.unsqueeze(1),
                                                Bc.unsqueeze(1), Cc.unsqueeze(1),
                                                A_real, A_imag, track, state=state,
                                                delta_softplus=True)
             y = y.squeeze(1) + x_branch * self.D
+            if rank1:
+                beta = self._compact_beta(x_dt, x_branch, Bc)
         else:
             y, (h, beta) = hip_step(x_dt, x_branch, Bc, Cc, A_real, A_imag, track, self.D,
-                                    state, delta_softplus=True)
+                                    state, delta_softplus=True, compact=rank1)
         out = self.out_proj(y * F.silu(z))
         return out, (h, beta)
 
@@ -324,14 +345,16 @@ class Mamba(nn.Module):
             x = self.norm_f(x)
         return x, new_cache
 
-    def prime_cache(self, input_ids):
+    def prime_cache(self, input_ids, compact=False):
         """Full causal forward returning (norm_f(last hidden), per-layer cache)
-        (engine/mamba.py:603-620), the scans on HIP with the final state."""
+        (engine/mamba.py:603-620), the scans on HIP with the final state.
+        compact=True keeps each layer's beta in rank-1 rows (see
+        Mamba3Block.forward_with_state)."""
         assert not self.config.bidirectional, "prime_cache() requires a causal model"
         cur = self.embedding(input_ids)
         cache = []
         for layer in self.layers:
-            mixed, st = layer["mixer"].forward_with_state(layer["norm"](cur))
+            mixed, st = layer["mixer"].forward_with_state(layer["norm"](cur), compact=compact)
             cur = cur + mixed
             cache.append(st)
         return self.norm_f(cur[:, -1, :]), cache

@@ -91,15 +91,17 @@ class SearchMamba(nn.Module):
 
     # ── O(1) cached evaluation ──
 
-    def prime_board(self, board_encoding):
+    def prime_board(self, board_encoding, compact=False):
         """Encode one board (ids (L,) or (1, L), list or tensor) and return
-        (final_hidden, cache) for step() (engine/search_mamba.py:162-175)."""
+        (final_hidden, cache) for step() (engine/search_mamba.py:162-175).
+        compact=True keeps each layer's beta in rank-1 rows [dt*u | B]
+        (half the state bytes per step; same results)."""
         if not torch.is_tensor(board_encoding):
             board_encoding = torch.as_tensor(board_encoding, dtype=torch.long,
                                              device=self._device())
         if board_encoding.dim() == 1:
             board_encoding = board_encoding.unsqueeze(0)
-        return self.backbone.prime_cache(board_encoding)
+        return self.backbone.prime_cache(board_encoding, compact=compact)
 
     @staticmethod
     def _expand_cache(cache, k):

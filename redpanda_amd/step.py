@@ -10,6 +10,13 @@ states, engine/mars_search.py:222-224, engine/search_mamba.py:177-187), unless
 A state that is an expanded view of one (D, N) state -- a batch-1 cache
 fanned out to R rollouts, as SearchMamba._expand_cache returns it -- is read
 in place by every rollout (no copies).
+
+Compact states: beta_t = (dt_t u_t) outer B_t is rank-1, so a cache may carry
+it as rows [dt*u | B] of D + N floats (`(h, bp)` with bp (R, D + N)) instead
+of (R, D, N).  The step then moves half the bytes and returns the same
+format; results are the same bits as with the full form, since beta_prev is
+formed by the multiply that produced it.  `compact_beta` builds such a row
+from a step's inputs; `full_beta` expands one back.
 """
 
 import ctypes
@@ -28,21 +35,39 @@ def _rows(t):
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def is_compact(beta):
+    """Whether a cached beta is in the rank-1 row form (R, D + N)."""
+    return beta.dim() == 2
+
+
+def compact_beta(dtu, Bc):
+    """Rank-1 rows [dt*u | B] (fp32, (R, D + N)) of beta = (dt*u) outer B."""
+    return torch.cat([dtu.to(torch.float32), Bc.to(torch.float32)], dim=-1)
+
+
+def full_beta(bp, D):
+    """The (R, D, N) beta of rank-1 rows bp (R, D + N): (dt*u)[:, :, None] * B[:, None, :]."""
+    return bp[..., :D, None] * bp[..., None, D:]
+
+
 def _state_pair(h, b, R, D, N):
-    """(h, beta, broadcast) for the kernel: per-rollout contiguous states, or
-    one shared (D, N) state when both are stride-0 expansions of one."""
-    if h.shape != (R, D, N) or b.shape != (R, D, N):
-        raise ValueError(f"step: state must be (R, D, N) = {(R, D, N)}")
+    """(h, beta, broadcast, rank1) for the kernel: per-rollout contiguous
+    states, or one shared state when both are stride-0 expansions of one;
+    beta full (R, D, N) or in rank-1 rows (R, D + N)."""
+    rank1 = is_compact(b)
+    bshape = (R, D + N) if rank1 else (R, D, N)
+    if h.shape != (R, D, N) or b.shape != bshape:
+        raise ValueError(f"step: state must be h {(R, D, N)} and beta {bshape}")
     h = h.to(torch.float32)
     b = b.to(torch.float32)
     if R > 1 and h.stride(0) == 0 and b.stride(0) == 0 and h[0].is_contiguous() and \
             b[0].is_contiguous():
-        return h, b, 1
-    return h.contiguous(), b.contiguous(), 0
+        return h, b, 1, rank1
+    return h.contiguous(), b.contiguous(), 0, rank1
 
 
 def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None,
-             delta_softplus=False):
+             delta_softplus=False, compact=False):
     """One step for R rollouts.
 
     delta, u: (R, D); Bc, Cc: (R, N) (contracted over p); A_real/A_imag:
@@ -50,7 +75,8 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     fp32 (R, D, N) (or an expansion of one (1, D, N) state) or None for a
     fresh state.  Returns (y (R, D) incl. u*D, (h_new, beta_new)).  With
     delta_softplus, `delta` is the dt projection x and the step uses
-    F.softplus(x) (engine/mamba.py:300).
+    F.softplus(x) (engine/mamba.py:300).  beta in rank-1 rows (R, D + N)
+    returns rank-1 rows; with no state, `compact` chooses the form returned.
     """
     lib = _lib.load()
     R, D = u.shape
@@ -69,11 +95,13 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     Dk = _f32c(Dskip.detach())
     h_in = beta_in = None
     broadcast = 0
+    rank1 = bool(compact)
     if state is not None:
-        h_in, beta_in, broadcast = _state_pair(state[0], state[1], R, D, N)
+        h_in, beta_in, broadcast, rank1 = _state_pair(state[0], state[1], R, D, N)
     if out is None:
         h_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
-        beta_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
+        beta_out = torch.empty((R, D + N) if rank1 else (R, D, N), dtype=torch.float32,
+                               device=dev)
         y = torch.empty((R, D), dtype=torch.float32, device=dev)
     else:
         y, h_out, beta_out = out
@@ -89,5 +117,6 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     a.h_out, a.beta_out, a.y = h_out.data_ptr(), beta_out.data_ptr(), y.data_ptr()
     a.broadcast_state = broadcast
     a.delta_softplus = 1 if delta_softplus else 0
+    a.beta_rank1 = 1 if rank1 else 0
     _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
     return y, (h_out, beta_out)

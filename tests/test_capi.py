@@ -150,6 +150,26 @@ def test_step_broadcast_state_rules(lib):
     assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "beta_out": 0x200000 - 64}))) < 0
 
 
+def test_step_rank1_rules(lib):
+    """Rank-1 beta rows (R, D + N): flags validated; beta_out may not overlap
+    beta_in, since every channel tile of a rollout reads its B_prev part."""
+    R, D, N = 16, 64, 20
+    ok = dict(beta_rank1=1, h_in=0x100000, beta_in=0x200000, h_out=0x300000,
+              beta_out=0x400000)
+    assert lib.rp_step_check(ctypes.byref(_step_args(**ok))) == 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "beta_rank1": 2}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "reserved": 1}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "beta_out": 0x200000}))) < 0
+    assert "rank-1" in lib.rp_last_error().decode()
+    # the input rows end at beta_in + R (D + N) 4 bytes
+    end = 0x200000 + R * (D + N) * 4
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "beta_out": end}))) == 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "beta_out": end - 4}))) < 0
+    # broadcast: one shared (D + N) row
+    bc = dict(ok, broadcast_state=1)
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**bc, "beta_out": 0x200000 + (D + N) * 4}))) == 0
+
+
 def test_initial_state_rules(lib):
     f = 0x10000
     assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f))) == 0
