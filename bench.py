@@ -290,28 +290,6 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
         for a, _ in per_layer:
             _lib.check(lib.rp_step(ctypes.byref(a), stream), lib)
 
-    for _ in range(max(args.warmup, 1)):
-        ply()
-    torch.cuda.synchronize()
-    if not keep:  # counter pass: the warm-up dispatches are the sample
-        return layers * max(args.warmup, 1)
-    t0 = time.perf_counter()
-    for _ in range(plies):
-        ply()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    timer = EventTimer(torch)
-    t_launch = timer.time(ply, plies) / layers
-    nb = step_bytes(R, D, N, NR, NT)
-    # the first ply after a batch-1 cache is fanned out to the R rollouts:
-    # every rollout reads the one shared state (no expand copies)
-    a0, keep0 = per_layer[0]
-    shared_h = torch.randn((1, D, N), generator=gen).to(dev)
-    shared_b = torch.randn((1, D, N), generator=gen).to(dev)
-    ab = _lib.StepArgs.from_buffer_copy(a0)
-    ab.h_in, ab.beta_in, ab.broadcast_state = shared_h.data_ptr(), shared_b.data_ptr(), 1
-    t_shared = timer.time(lambda: _lib.check(lib.rp_step(ctypes.byref(ab), stream), lib), 10)
-    nb_shared = R * (8 * D * N + 12 * D + 8 * N) + 8 * D * N + (2 * D * NR + D * NT + D) * 4
     # the same plies with the cache's beta in rank-1 rows (R, D + N): the
     # rows ping-pong between two buffers (a rank-1 step may not update them
     # in place); h is updated in place as above
@@ -333,6 +311,31 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
             _lib.check(lib.rp_step(ctypes.byref(pair[i]), stream), lib)
         parity[0] = 1 - i
 
+    for _ in range(max(args.warmup, 1)):
+        ply()
+    torch.cuda.synchronize()
+    if not keep:  # counter pass: the warm-up dispatches are the sample
+        for _ in range(max(args.warmup, 1)):
+            ply_compact()
+        torch.cuda.synchronize()
+        return layers * max(args.warmup, 1)
+    t0 = time.perf_counter()
+    for _ in range(plies):
+        ply()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    timer = EventTimer(torch)
+    t_launch = timer.time(ply, plies) / layers
+    nb = step_bytes(R, D, N, NR, NT)
+    # the first ply after a batch-1 cache is fanned out to the R rollouts:
+    # every rollout reads the one shared state (no expand copies)
+    a0, keep0 = per_layer[0]
+    shared_h = torch.randn((1, D, N), generator=gen).to(dev)
+    shared_b = torch.randn((1, D, N), generator=gen).to(dev)
+    ab = _lib.StepArgs.from_buffer_copy(a0)
+    ab.h_in, ab.beta_in, ab.broadcast_state = shared_h.data_ptr(), shared_b.data_ptr(), 1
+    t_shared = timer.time(lambda: _lib.check(lib.rp_step(ctypes.byref(ab), stream), lib), 10)
+    nb_shared = R * (8 * D * N + 12 * D + 8 * N) + 8 * D * N + (2 * D * NR + D * NT + D) * 4
     for _ in range(max(args.warmup, 1)):
         ply_compact()
     torch.cuda.synchronize()
@@ -648,6 +651,26 @@ def profile_pass(torch):
     dst = torch.empty_like(src)
     torch.neg(src, out=dst)
     torch.cuda.synchronize()
+    # the BCNorm prologue at the layer shape (bf16 projections), three each way
+    from redpanda_amd.bcnorm import make_bcnorm_args
+    T, Nn, P = SCAN_SHAPE["B"] * SCAN_SHAPE["L"], SCAN_SHAPE["NR"] + SCAN_SHAPE["NT"], 4
+    xd = torch.randn(T, 48 + 2 * Nn * P, device=dev).to(torch.bfloat16)
+    Bx, Cx = xd[:, 48:48 + Nn * P], xd[:, 48 + Nn * P:]
+    wB, wC = torch.ones(Nn * P, device=dev), torch.ones(Nn * P, device=dev)
+    bo = [torch.empty(T, Nn, device=dev), torch.empty(T, Nn, device=dev)]
+    ba = make_bcnorm_args(Bx, Cx, wB, wC, Nn, P, 1e-5, True, bo[0], bo[1])
+    bg_t = [torch.randn(T, Nn, device=dev), torch.randn(T, Nn, device=dev),
+            torch.empty(T, Nn * P, dtype=torch.bfloat16, device=dev),
+            torch.empty(T, Nn * P, dtype=torch.bfloat16, device=dev),
+            torch.empty(Nn * P, device=dev), torch.empty(Nn * P, device=dev),
+            torch.empty(max(lib.rp_bcnorm_work_bytes(ctypes.byref(ba)), 256), dtype=torch.uint8,
+                        device=dev)]
+    bgr = _lib.BcNormGrad(*(t.data_ptr() for t in bg_t[:6]), bg_t[6].data_ptr(), bg_t[6].numel())
+    for _ in range(3):
+        _lib.check(lib.rp_bcnorm_fwd(ctypes.byref(ba), stream), lib)
+        _lib.check(lib.rp_bcnorm_bwd(ctypes.byref(ba), ctypes.byref(bgr), stream), lib)
+    torch.cuda.synchronize()
+    del xd, bo, bg_t
     print(f"[bench] profile pass done: scan fwd/bwd x3, step x{step_layers}, "
           f"calibration neg {src.numel() * 4} bytes each way", file=sys.stderr, flush=True)
 

@@ -456,12 +456,14 @@ int rp_step(const rp_step_args* a, void* stream) {
     // rollouts per workgroup: a few amortise the workgroup's prologue (gate
     // parameters, B / C rows) while keeping many workgroups in flight;
     // measured at 4096 rollouts x 1024 channels, d_state 20: 4 per workgroup
-    // (4096 workgroups) beat 1..3 and 6..32
+    // (4096 workgroups) beat 1..3 and 6..32 with the full beta; with rank-1
+    // rows (half the bytes per rollout) 8 beat 1..4 and 16
+    const int64_t ri_max = a->beta_rank1 ? 8 : 4;
     int64_t ri = step_ri_override();
     if (ri == 0) {
       ri = (a->R * (int64_t)p.ctiles) / 2048;
       if (ri < 1) ri = 1;
-      if (ri > 4) ri = 4;
+      if (ri > ri_max) ri = ri_max;
     }
     if (ri > rp::kStepRiMax) return fail(RP_ERR_UNSUPPORTED, "step: rollouts per workgroup");
     p.ri = (int)ri;

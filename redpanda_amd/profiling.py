@@ -25,8 +25,35 @@ import sys
 CALIB_MARK = "neg_kernel"  # substring of the calibration dispatch's full name
 
 
+def _template_args(kernel_name):
+    """Top-level template arguments of a demangled kernel name."""
+    start = kernel_name.find("<")
+    if start < 0:
+        return []
+    depth, cur, args = 0, [], []
+    for ch in kernel_name[start:]:
+        if ch == "<":
+            depth += 1
+            if depth == 1:
+                continue
+        elif ch == ">":
+            depth -= 1
+            if depth == 0:
+                args.append("".join(cur).strip())
+                break
+        elif ch == "," and depth == 1:
+            args.append("".join(cur).strip())
+            cur = []
+            continue
+        cur.append(ch)
+    return args
+
+
 def short_name(kernel_name):
-    """`void rp::scan_bwd_kernel<8, 5, ...>(rp::ScanParams, ...)` -> `scan_bwd_kernel`."""
+    """`void rp::scan_bwd_kernel<8, 5, ...>(rp::ScanParams, ...)` -> `scan_bwd_kernel`.
+    The step tile kernel's rank-1 instantiation (last template argument
+    RANK1 = true) is `step_tile_kernel[rank1]`, so the two forms' counters
+    stay apart."""
     name = kernel_name
     depth, out = 0, []
     for ch in name:  # drop template arguments
@@ -38,7 +65,12 @@ def short_name(kernel_name):
             out.append(ch)
     name = "".join(out).split("(")[0]
     name = name.replace("void ", "").strip()
-    return re.sub(r"^.*::", "", name)
+    name = re.sub(r"^.*::", "", name)
+    if name == "step_tile_kernel":
+        args = _template_args(kernel_name)
+        if len(args) == 6 and args[-1] in ("true", "1"):
+            name += "[rank1]"
+    return name
 
 
 def counter_means(path, counter):
@@ -93,8 +125,11 @@ def valu(csv_path):
             "kernels": out}
 
 
-def stats_markdown(csv_path, cmd, title):
+def stats_markdown(csv_path, cmd, title, top=None):
     rows = list(csv.DictReader(open(csv_path)))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    if top:
+        rows = rows[:top]
     lines = [f"# {title}", "", "Command (repo root, one MI355X):", "", f"    {cmd}", "",
              "| kernel | calls | avg (us) | min (us) | max (us) | share |",
              "|---|---|---|---|---|---|"]
@@ -115,6 +150,7 @@ def main(argv=None):
     s.add_argument("csv")
     s.add_argument("--cmd", required=True)
     s.add_argument("--title", default="rocprofv3 kernel statistics")
+    s.add_argument("--top", type=int, default=None, help="only the N kernels with most total time")
     t = sub.add_parser("traffic")
     t.add_argument("--fetch", required=True)
     t.add_argument("--write", required=True)
@@ -125,7 +161,7 @@ def main(argv=None):
     v.add_argument("--out")
     a = ap.parse_args(argv)
     if a.action == "stats":
-        sys.stdout.write(stats_markdown(a.csv, a.cmd, a.title))
+        sys.stdout.write(stats_markdown(a.csv, a.cmd, a.title, a.top))
     elif a.action == "valu":
         text = json.dumps(valu(a.csv), indent=1, sort_keys=True)
         if a.out:
