@@ -68,6 +68,8 @@ def parse():
     ap.add_argument("--no-step", action="store_true", help="skip the step() workload")
     ap.add_argument("--no-long", action="store_true",
                     help="skip the long-sequence (L=2048) scan line")
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer comparison")
+    ap.add_argument("--no-mixer", action="store_true", help="skip the mixer-gate kernels")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--profile-pass", action="store_true",
@@ -592,6 +594,9 @@ def measured_traffic():
     if "scan_bwd_kernel" in k:
         out["scan_bwd_kernel+reductions"] = sum(
             k[n]["bytes"] for n in ("scan_bwd_kernel", "bwd_reduce_bc", "bwd_reduce_par") if n in k)
+    if "mixer_out_bwd_vec_kernel" in k:
+        out["mixer_out_bwd+reduction"] = sum(
+            k[n]["bytes"] for n in ("mixer_out_bwd_vec_kernel", "mixer_out_reduce_kernel") if n in k)
     return out
 
 
@@ -803,16 +808,19 @@ def main():
         lng = bench_long(torch, args)
         print(f"[bench] long: {lng['tok_s']:.4g} tokens/s; fwd {lng['t_fwd'] * 1e3:.2f} ms, "
               f"bwd {lng['t_bwd'] * 1e3:.2f} ms", file=sys.stderr, flush=True)
-    lay = bench_layer(torch, args)
-    print(f"[bench] layer fwd+bwd: fused {lay['t_fused'] * 1e3:.3f} ms "
-          f"({lay['tok_fused']:.4g} tokens/s); scan-only drop-in {lay['t_dropin'] * 1e3:.3f} ms "
-          f"({lay['tok_dropin']:.4g} tokens/s)", file=sys.stderr, flush=True)
-    mix = bench_mixer(torch, args)
-    print(f"[bench] mixer gate: fwd {mix['t_fwd'] * 1e6:.1f} us "
-          f"({mix['fwd_bytes'] / mix['t_fwd'] / 1e9:.0f} GB/s), bwd {mix['t_bwd'] * 1e6:.1f} us "
-          f"({mix['bwd_bytes'] / mix['t_bwd'] / 1e9:.0f} GB/s); fwd+bwd autograd "
-          f"{mix['t_fused'] * 1e6:.1f} us fused vs {mix['t_torch'] * 1e6:.1f} us torch ops",
-          file=sys.stderr, flush=True)
+    lay = mix = None
+    if not args.no_layer:
+        lay = bench_layer(torch, args)
+        print(f"[bench] layer fwd+bwd: fused {lay['t_fused'] * 1e3:.3f} ms "
+              f"({lay['tok_fused']:.4g} tokens/s); scan-only drop-in {lay['t_dropin'] * 1e3:.3f} ms "
+              f"({lay['tok_dropin']:.4g} tokens/s)", file=sys.stderr, flush=True)
+    if not args.no_mixer:
+        mix = bench_mixer(torch, args)
+        print(f"[bench] mixer gate: fwd {mix['t_fwd'] * 1e6:.1f} us "
+              f"({mix['fwd_bytes'] / mix['t_fwd'] / 1e9:.0f} GB/s), bwd {mix['t_bwd'] * 1e6:.1f} us "
+              f"({mix['bwd_bytes'] / mix['t_bwd'] / 1e9:.0f} GB/s); fwd+bwd autograd "
+              f"{mix['t_fused'] * 1e6:.1f} us fused vs {mix['t_torch'] * 1e6:.1f} us torch ops",
+              file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -873,7 +881,8 @@ def main():
                 "avg_launch_s": step["t_launch_rank1"],
                 "alg_bytes_per_launch": step["bytes_rank1"],
                 "achieved_GBps": step["GBps_rank1"],
-                "frac": step["GBps_rank1"] / HBM_PEAK_GBS},
+                "frac": step["GBps_rank1"] / HBM_PEAK_GBS,
+                "traffic": tr.get("step_tile_kernel[rank1]")},
             "from_shared_state": {
                 "workload": "first ply after a batch-1 cache is fanned out to the rollouts "
                             "(broadcast input state, no copies)",
@@ -888,33 +897,35 @@ def main():
             "fwd_s": lng["t_fwd"], "bwd_s": lng["t_bwd"],
             "alg_bytes_fwd": lng["fwd_bytes"], "alg_bytes_bwd": lng["bwd_bytes"],
         }
-    line["layer"] = {
-        "metric": "tokens/s", "value": lay["tok_fused"],
-        "config": {"workload": "one bidirectional Mamba3Block forward + backward under bf16 "
-                               "autocast (projections on hipBLASLt, SSM path fused HIP)",
-                   **LAYER_SHAPE, "mimo_p": 4},
-        "fwd_bwd_s": lay["t_fused"],
-        "scan_only_dropin": {"workload": "the reference's layer ops with only the scan "
-                                         "swapped for the HIP scan",
-                             "fwd_bwd_s": lay["t_dropin"], "tokens_s": lay["tok_dropin"]},
-    }
-    line["mixer_gate"] = {
-        "workload": "(y + 2 u D) silu(z) of the bidirectional layer at the scan shape, "
-                    "bf16 u / z (z a chunk of the in_proj output), fp32 y and gradients",
-        "fwd": {"kernel": "mixer_out_fwd_kernel", "avg_launch_s": mix["t_fwd"],
-                "alg_bytes_per_launch": mix["fwd_bytes"],
-                "achieved_GBps": mix["fwd_bytes"] / mix["t_fwd"] / 1e9,
-                "frac": mix["fwd_bytes"] / mix["t_fwd"] / 1e9 / HBM_PEAK_GBS,
-                "traffic": tr.get("mixer_out_fwd_kernel")},
-        "bwd": {"kernel": "mixer_out_bwd_kernel + reduction", "avg_launch_s": mix["t_bwd"],
-                "alg_bytes_per_launch": mix["bwd_bytes"],
-                "achieved_GBps": mix["bwd_bytes"] / mix["t_bwd"] / 1e9,
-                "frac": mix["bwd_bytes"] / mix["t_bwd"] / 1e9 / HBM_PEAK_GBS,
-                "traffic": tr.get("mixer_out_bwd_kernel")},
-        "timing": "each launch after a 512 MB read that displaces the last-level cache",
-        "warm_cache_avg_launch_s": {"fwd": mix["t_fwd_warm"], "bwd": mix["t_bwd_warm"]},
-        "fwd_bwd_autograd_s": {"fused": mix["t_fused"], "torch_ops": mix["t_torch"]},
-    }
+    if lay is not None:
+        line["layer"] = {
+            "metric": "tokens/s", "value": lay["tok_fused"],
+            "config": {"workload": "one bidirectional Mamba3Block forward + backward under bf16 "
+                                   "autocast (projections on hipBLASLt, SSM path fused HIP)",
+                       **LAYER_SHAPE, "mimo_p": 4},
+            "fwd_bwd_s": lay["t_fused"],
+            "scan_only_dropin": {"workload": "the reference's layer ops with only the scan "
+                                             "swapped for the HIP scan",
+                                 "fwd_bwd_s": lay["t_dropin"], "tokens_s": lay["tok_dropin"]},
+        }
+    if mix is not None:
+        line["mixer_gate"] = {
+            "workload": "(y + 2 u D) silu(z) of the bidirectional layer at the scan shape, "
+                        "bf16 u / z (z a chunk of the in_proj output), fp32 y and gradients",
+            "fwd": {"kernel": "mixer_out_fwd_vec_kernel", "avg_launch_s": mix["t_fwd"],
+                    "alg_bytes_per_launch": mix["fwd_bytes"],
+                    "achieved_GBps": mix["fwd_bytes"] / mix["t_fwd"] / 1e9,
+                    "frac": mix["fwd_bytes"] / mix["t_fwd"] / 1e9 / HBM_PEAK_GBS,
+                    "traffic": tr.get("mixer_out_fwd_vec_kernel")},
+            "bwd": {"kernel": "mixer_out_bwd_vec_kernel + reduction", "avg_launch_s": mix["t_bwd"],
+                    "alg_bytes_per_launch": mix["bwd_bytes"],
+                    "achieved_GBps": mix["bwd_bytes"] / mix["t_bwd"] / 1e9,
+                    "frac": mix["bwd_bytes"] / mix["t_bwd"] / 1e9 / HBM_PEAK_GBS,
+                    "traffic": tr.get("mixer_out_bwd+reduction")},
+            "timing": "each launch after a 512 MB read that displaces the last-level cache",
+            "warm_cache_avg_launch_s": {"fwd": mix["t_fwd_warm"], "bwd": mix["t_bwd_warm"]},
+            "fwd_bwd_autograd_s": {"fused": mix["t_fused"], "torch_ops": mix["t_torch"]},
+        }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)
 
