@@ -733,6 +733,43 @@ def cpu_baseline(budget_s):
             "torch": torch.__version__}
 
 
+def cpu_layer_baseline(budget_s):
+    """The reference's layer on the CPU: the oracle's restatement of
+    Mamba3Block (engine/mamba.py:141-380, its PyTorch scan path), fp32
+    forward + backward at the layer shape with a reduced batch."""
+    import torch
+    from oracle import model_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    sh = LAYER_SHAPE
+    Bs = 4
+    torch.manual_seed(0)
+    cfg = model_ref.MambaConfig(d_model=sh["d_model"], n_layer=1, d_state=sh["d_state"],
+                                n_track_state=sh["n_track"], bidirectional=True)
+    blk = model_ref.Mamba3Block(cfg)
+    x = torch.randn(Bs, sh["L"], sh["d_model"])
+
+    def run():
+        blk.zero_grad(set_to_none=True)
+        blk(x).square().mean().backward()
+
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * budget_s:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": Bs * sh["L"] / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"oracle fp32 restatement of the reference's Mamba3Block on the CPU "
+                       f"(its PyTorch scan path), bidirectional fwd+bwd, B={Bs} L={sh['L']} "
+                       f"d_model={sh['d_model']} N={sh['d_state']}; median of {len(times)} runs")}
+
+
 def cpu_step_baseline(budget_s):
     """The reference's per-layer torch step (engine/mamba.py:466-494; the
     oracle's fp32 restatement) at the step workload's layer shape over all
@@ -827,6 +864,10 @@ def main():
         cpu = cpu_baseline(args.cpu_seconds)
         print(f"[bench] cpu: {cpu['value']:.4g} tokens/s on {cpu['cores']} threads",
               file=sys.stderr, flush=True)
+        if lay is not None:
+            lay["cpu_baseline"] = cpu_layer_baseline(args.cpu_seconds / 3)
+            print(f"[bench] cpu layer: {lay['cpu_baseline']['value']:.4g} tokens/s",
+                  file=sys.stderr, flush=True)
         if step is not None:
             step["cpu_baseline"] = cpu_step_baseline(args.cpu_seconds / 3)
             print(f"[bench] cpu step: {step['cpu_baseline']['value']:.4g} rollout-steps/s",
@@ -907,6 +948,7 @@ def main():
             "scan_only_dropin": {"workload": "the reference's layer ops with only the scan "
                                              "swapped for the HIP scan",
                                  "fwd_bwd_s": lay["t_dropin"], "tokens_s": lay["tok_dropin"]},
+            "cpu_baseline": lay.get("cpu_baseline"),
         }
     if mix is not None:
         line["mixer_gate"] = {
