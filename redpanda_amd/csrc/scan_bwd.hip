@@ -476,14 +476,18 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 }
 
 // dB / dC: sum the per-tile partials in a fixed order (fp64 accumulator).
+// The loads do not depend on the sum, so the unrolled loop keeps 8 of them in
+// flight while the additions stay in tile order.
 __global__ void bwd_reduce_bc(const float* __restrict__ part, float* __restrict__ dB,
                               float* __restrict__ dC, int64_t per, int ntiles) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= 2 * per) return;
   const int which = e >= per;
   const int64_t k = which ? e - per : e;
+  const float* src = part + (int64_t)which * ntiles * per + k;
   double acc = 0.0;
-  for (int g = 0; g < ntiles; ++g) acc += part[((int64_t)which * ntiles + g) * per + k];
+#pragma unroll 8
+  for (int g = 0; g < ntiles; ++g) acc += src[(int64_t)g * per];
   (which ? dC : dB)[k] = (float)acc;
 }
 
@@ -496,6 +500,7 @@ __global__ void bwd_reduce_par(const double* __restrict__ part, float* __restric
   if (e >= DN) return;
   const int c = (int)(e / N), n = (int)(e % N);
   double a = 0.0, bsum = 0.0;
+#pragma unroll 8
   for (int g = 0; g < nbg; ++g) {
     a += part[(int64_t)g * 2 * DN + e];
     bsum += part[(int64_t)g * 2 * DN + DN + e];
