@@ -106,3 +106,20 @@ def test_step_softplus(gpu_lib, R, D, NR, NT):
     assert nrel(y, yr) <= 1e-6 and nrel(h, hr) <= 1e-6 and nrel(b, br) <= 1e-6
     print(f"[softplus step] R={R} D={D} h bitwise {float((h == hr).float().mean()):.6f}",
           flush=True)
+
+
+@pytest.mark.parametrize("bidirectional", [False, True])
+def test_inference_forward_equals_training_forward(gpu_lib, bidirectional):
+    """Without checkpoints (no autograd) every direction applies softplus on
+    load; with them the forward direction caches softplus(x) and the reverse
+    direction reads the cache: the same bits either way."""
+    B, L, D, NR, NT = 3, 37, 160, 32, 8
+    ins = _inputs(B, L, D, NR, NT, seed=41, dt=torch.bfloat16)
+    with torch.no_grad():
+        y_inf = hip_trapezoidal_scan(*ins, NR, NR + NT, bidirectional=bidirectional,
+                                     delta_softplus=True)
+    a = _leaves(ins)
+    y_tr = hip_trapezoidal_scan(*a, NR, NR + NT, bidirectional=bidirectional,
+                                delta_softplus=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y_inf, y_tr.detach())
