@@ -355,6 +355,61 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
                 bytes_rank1=nb_c, GBps_rank1=nb_c / t_launch_c / 1e9)
 
 
+# The whole search-model ply of the step workload: 8 causal layers, d_model
+# 512, d_state 16 + 4, mimo_p 2 (the search model's), 4096 rollouts.
+PLY_SHAPE = dict(R=4096, layers=8, d_model=512, d_state=20, n_track=4, mimo_p=2)
+
+
+def bench_ply(torch, args, plies=8):
+    """Whole plies through Mamba.step(input_embed=...) (projections on
+    hipBLASLt, norms, the fused step kernel per layer), fp32, no autograd:
+    the reference's cache format and rank-1 beta rows."""
+    from redpanda_amd import mamba as hm
+    sh = PLY_SHAPE
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = hm.MambaConfig(d_model=sh["d_model"], n_layer=sh["layers"], d_state=sh["d_state"],
+                         n_track_state=sh["n_track"], mimo_p=sh["mimo_p"], vocab_size=64)
+    model = hm.Mamba(cfg).to(dev).eval()
+    gen = torch.Generator(device=dev).manual_seed(1011)
+    emb = torch.randn(plies, sh["R"], sh["d_model"], generator=gen, device=dev)
+    out = {}
+    with torch.no_grad():
+        for name, compact in (("full", False), ("rank1", True)):
+            cache = None
+            for k in range(2):  # warm-up plies build the cache
+                _, cache = model.step(input_embed=emb[k], cache=cache, compact=compact)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for k in range(plies):
+                _, cache = model.step(input_embed=emb[k], cache=cache, compact=compact)
+            torch.cuda.synchronize()
+            dt = (time.perf_counter() - t0) / plies
+            out[name] = dict(s_per_ply=dt, rollout_steps_s=sh["R"] / dt)
+            del cache
+    return out
+
+
+def practical_hbm_peak(torch):
+    """GB/s of a 1 GiB device-to-device copy (read + write), best of 5."""
+    dev = torch.device("cuda:0")
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(5):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3
+        best = t if best is None else min(best, t)
+    return 2 * src.numel() * 4 / best / 1e9
+
+
 def mixer_inputs(torch, dev, seed):
     """The mixer gate's operands at the scan shape: y fp32 from the scan,
     u bf16, z bf16 as the second half of a (B, L, 2 d_inner) in_proj output."""
@@ -845,6 +900,15 @@ def main():
         lng = bench_long(torch, args)
         print(f"[bench] long: {lng['tok_s']:.4g} tokens/s; fwd {lng['t_fwd'] * 1e3:.2f} ms, "
               f"bwd {lng['t_bwd'] * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    ply = None
+    if not args.no_step:
+        ply = bench_ply(torch, args)
+        print(f"[bench] whole ply ({PLY_SHAPE['layers']} layers, R={PLY_SHAPE['R']}): "
+              f"{ply['full']['s_per_ply'] * 1e3:.3f} ms ({ply['full']['rollout_steps_s']:.4g} "
+              f"rollout-steps/s); rank-1 cache {ply['rank1']['s_per_ply'] * 1e3:.3f} ms "
+              f"({ply['rank1']['rollout_steps_s']:.4g})", file=sys.stderr, flush=True)
+    hbm_practical = practical_hbm_peak(torch)
+    print(f"[bench] torch 1 GiB copy: {hbm_practical:.0f} GB/s", file=sys.stderr, flush=True)
     lay = mix = None
     if not args.no_layer:
         lay = bench_layer(torch, args)
@@ -888,6 +952,9 @@ def main():
         key = "scan_bwd_kernel" if k["kernel"].startswith("scan_bwd") else "scan_fwd_kernel"
         k["valu"] = valu_roofline(vc.get(key), k["seconds"]) if k["traffic_key"] else None
     roof["valu"] = dom.get("valu")
+    # torch's 1 GiB device-to-device copy (read + write); the step kernel's
+    # coalesced non-temporal streaming runs above it
+    roof["torch_copy_GBps"] = hbm_practical
     ms = sc["elapsed"] / args.steps * 1e3
     line = {
         "metric": "scan fwd+bwd tokens/s & %HBM peak; batched step() rollout-steps/s",
@@ -915,6 +982,14 @@ def main():
                          "alg_bytes_per_launch": step["bytes"],
                          "avg_launch_s": step["t_launch"]},
             "cpu_baseline": step.get("cpu_baseline"),
+            "whole_ply": None if ply is None else {
+                "workload": "Mamba.step(input_embed) over 8 causal layers, d_model 512, "
+                            "mimo_p 2, 4096 rollouts, fp32, no autograd (projections, norms "
+                            "and the fused step kernel)",
+                "rollout_steps_s": ply["full"]["rollout_steps_s"],
+                "s_per_ply": ply["full"]["s_per_ply"],
+                "rank1_cache": {"rollout_steps_s": ply["rank1"]["rollout_steps_s"],
+                                "s_per_ply": ply["rank1"]["s_per_ply"]}},
             "rank1_cache": {
                 "workload": "the same plies with each layer's beta cached as rank-1 rows "
                             "[dt*u | B] (D + N floats per rollout; bit-identical results)",

@@ -325,8 +325,11 @@ class Mamba(nn.Module):
         """An empty per-layer cache (engine/mamba.py:560-562)."""
         return [None] * len(self.layers)
 
-    def step(self, token_id=None, cache=None, input_embed=None, apply_final_norm=True):
-        """One token through every layer (engine/mamba.py:564-601)."""
+    def step(self, token_id=None, cache=None, input_embed=None, apply_final_norm=True,
+             compact=False):
+        """One token through every layer (engine/mamba.py:564-601).  A layer
+        with no cached state starts from zero and, with compact=True, returns
+        its beta in rank-1 rows (see Mamba3Block.step)."""
         assert not self.config.bidirectional, "step() requires a causal model"
         if input_embed is not None:
             x = input_embed
@@ -338,7 +341,7 @@ class Mamba(nn.Module):
             cache = [None] * len(self.layers)
         new_cache = []
         for i, layer in enumerate(self.layers):
-            out, st = layer["mixer"].step(layer["norm"](x), cache[i])
+            out, st = layer["mixer"].step(layer["norm"](x), cache[i], compact=compact)
             x = x + out
             new_cache.append(st)
         if apply_final_norm:

@@ -229,6 +229,29 @@ def test_model_step_equals_forward(gpu_lib):
     assert e_step <= 1e-6 and e_prime <= 1e-6 and e_next <= 1e-6
 
 
+@pytest.mark.parametrize("compact", [False, True])
+def test_search_shape_plies_equal_forward(gpu_lib, compact):
+    """The batched-step workload at its model shape (8 causal layers, d_model
+    512, d_state 16 + 4, mimo_p 2) on a row subset: 32 plies of step() with
+    input_embed reproduce Mamba.forward(input_embeds=(R, 32, 512)) (1e-6),
+    with the reference's cache format and with rank-1 beta rows."""
+    cfg = dict(d_model=512, n_layer=8, d_state=20, n_track_state=4, mimo_p=2, vocab_size=64)
+    hip, _ = _pair(cfg, seed=6)
+    hip.eval()
+    gen = torch.Generator().manual_seed(7)
+    emb = torch.randn(12, 32, 512, generator=gen).to(dev)
+    with torch.no_grad():
+        full = hip(None, input_embeds=emb)
+        cache, outs = None, []
+        for t in range(emb.shape[1]):
+            hdn, cache = hip.step(input_embed=emb[:, t], cache=cache, compact=compact)
+            assert all(c[1].dim() == (2 if compact else 3) for c in cache)
+            outs.append(hdn)
+        e = rel(torch.stack(outs, 1), full)
+    print(f"32 plies vs forward (compact={compact}): {e:.1e}")
+    assert e <= 1e-6
+
+
 def test_step_under_autograd_matches_reference(gpu_lib):
     """Training through step() (SearchMamba.dynamics_rollout pattern): prime
     on a prefix, step T moves with autograd on, gradients of every parameter
