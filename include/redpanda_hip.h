@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 6
+#define RP_ABI_VERSION 7
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -133,6 +133,9 @@ typedef struct rp_scan_bwd_io {
  * rollout continues from -- a batch-1 cache fanned out to R rollouts without
  * the copies of engine/search_mamba.py:177-187 (expand().contiguous()); the
  * outputs must then not overlap the inputs.  0: the (R, D, N) layout above.
+ * z: with the gate branch given, y is returned already gated, y * silu(z)
+ * (the out_proj input of engine/mamba.py:497), silu rounded to z's dtype as
+ * torch rounds it.
  * beta_rank1 = 1: beta is carried by its rank-1 factors, since beta =
  * (dt u) outer B: beta_in / beta_out are (R, D + N) fp32 rows [dt*u | B]
  * (one (D + N) row with broadcast_state), and the step forms beta_prev =
@@ -159,6 +162,9 @@ typedef struct rp_step_args {
   int32_t delta_softplus;   /* 0 or 1: delta holds x, the step uses softplus(x) */
   int32_t beta_rank1;       /* 0 or 1, see above */
   int32_t reserved;         /* must be 0 */
+  const void* z;  int64_t z_sr;  /* NULL, or the (R, D) gate branch: y = y * silu(z) */
+  int32_t dtype_z;          /* RP_F32 / RP_BF16 / RP_F16 */
+  int32_t reserved2;        /* must be 0 */
 } rp_step_args;
 
 /*

@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -58,6 +58,7 @@ class StepArgs(ctypes.Structure):
         ("Dskip", _vp), ("h_out", _vp), ("beta_out", _vp), ("y", _vp),
         ("broadcast_state", _i32), ("delta_softplus", _i32),
         ("beta_rank1", _i32), ("reserved", _i32),
+        ("z", _vp), ("z_sr", _i64), ("dtype_z", _i32), ("reserved2", _i32),
     ]
 
 

@@ -396,6 +396,13 @@ int rp_step_check(const rp_step_args* a) {
     if (a->beta_rank1 && a->h_in && overlaps(a->beta_in, b_in_b, a->beta_out, b_out_b))
       return fail(RP_ERR_INVALID, "step args: rank-1 beta_out must not overlap beta_in");
   }
+  if (a->reserved2 != 0) return fail(RP_ERR_INVALID, "step args: reserved2 must be 0");
+  if (a->z != nullptr) {
+    if (a->dtype_z != RP_F32 && a->dtype_z != RP_BF16 && a->dtype_z != RP_F16)
+      return fail(RP_ERR_INVALID, "step args: unknown dtype code %d for z", a->dtype_z);
+    if (a->z_sr < a->D || !aligned(a->z, elem_size(a->dtype_z)))
+      return fail(RP_ERR_INVALID, "step args: z row stride shorter than D or z misaligned");
+  }
   if (a->NR > 0 && !a->A_real) return fail(RP_ERR_INVALID, "step args: NR>0 needs A_real");
   if (a->NR == 0 && a->A_imag) return fail(RP_ERR_INVALID, "step args: A_imag without NR");
   if (a->NT > 0 && !a->track) return fail(RP_ERR_INVALID, "step args: NT>0 needs track");
@@ -435,6 +442,9 @@ int rp_step(const rp_step_args* a, void* stream) {
   p.dsp = a->delta_softplus;
   p.rank1 = a->beta_rank1;
   p.bssr = a->broadcast_state ? 0 : a->D + a->N;
+  p.z = a->z;
+  p.zsr = a->z_sr;
+  p.dt_z = a->dtype_z;
   p.Ar = a->NR > 0 ? a->A_real : nullptr;
   p.Ai = a->NR > 0 ? a->A_imag : nullptr;
   p.Tk = a->NT > 0 ? a->track : nullptr;

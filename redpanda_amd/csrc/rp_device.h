@@ -75,6 +75,24 @@ __device__ __forceinline__ float fmul(float a, float b) { return a * b; }
 // delta = softplus(x) as torch computes it for the dt projection
 // (engine/mamba.py:300, F.softplus with beta 1, threshold 20, in fp32).
 __device__ __forceinline__ float softplus_of(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// fp32 -> the value a storage dtype holds (round to nearest even, as torch
+// converts); inf and nan pass through.
+__device__ __forceinline__ float round_storage(float v, int dtype) {
+  if (dtype == RP_F32) return v;
+  if (dtype == RP_BF16) {
+    uint32_t b = __float_as_uint(v);
+    if ((b & 0x7f800000u) != 0x7f800000u) b += 0x7fffu + ((b >> 16) & 1u);
+    return __uint_as_float(b & 0xffff0000u);
+  }
+  return static_cast<float>(static_cast<_Float16>(v));
+}
+
+// y * silu(z) as torch computes it: silu(z) = z / (1 + exp(-z)) rounded to
+// z's storage dtype, then the product in fp32.
+__device__ __forceinline__ float silu_gate(float y, float z, int dtype_z) {
+  return y * round_storage(z / (1.f + expf(-z)), dtype_z);
+}
 // The same derivative from delta = softplus(x) itself: sigmoid(x) =
 // 1 - exp(-delta), as -expm1(-delta) (accurate for small delta; 1 above the
 // threshold, where delta = x > 20).

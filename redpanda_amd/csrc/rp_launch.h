@@ -73,6 +73,9 @@ struct StepParams {
   int64_t ssr;  // elements between consecutive rollouts' input states (0: one shared state)
   int dsp;      // 1: delta holds x and the step uses softplus(x)
   int rank1;    // 1: beta as rows [dt*u | B] of D + N floats
+  const void* z;  // (R, D) gate branch or null: y = y * silu(z)
+  int64_t zsr;
+  int dt_z;
   int64_t bssr; // rank-1 input rows: elements between rollouts (0: one shared row)
   const float* Ar;
   const float* Ai;

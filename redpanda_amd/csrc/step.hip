@@ -90,7 +90,9 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
       }
     }
     if (s == 0) {
-      p.y[(int64_t)r * p.D + c] = y + fmul(uu, p.Dskip[c]);
+      float yv = y + fmul(uu, p.Dskip[c]);
+      if (p.z != nullptr) yv = silu_gate(yv, load_in(p.z, (int64_t)r * p.zsr + c, p.dt_z), p.dt_z);
+      p.y[(int64_t)r * p.D + c] = yv;
       if (p.rank1) p.beta_out[(int64_t)r * (p.D + p.N) + c] = fmul(dt, uu);
     }
   }
@@ -225,6 +227,8 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     float dt = p.delta[r * p.dsr + cld];
     if constexpr (DSP) dt = softplus_of(dt);
     const float uu = p.u[r * p.usr + cld];
+    // the gate branch, when y leaves gated
+    const float zz = p.z != nullptr ? load_in(p.z, r * p.zsr + cld, p.dt_z) : 0.f;
     // rank-1: the channel's (dt*u)_prev, halved as the scan halves dt*u
     float hdp = 0.f;
     if (p.h_in != nullptr) {
@@ -288,7 +292,9 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       ys[q] = ffma(hs, Cs[n], ys[q]);
     }
     if (cvalid) {
-      p.y[r * p.D + c] = tree_sum<S>(ys) + fmul(uu, dsk);
+      float yv = tree_sum<S>(ys) + fmul(uu, dsk);
+      if (p.z != nullptr) yv = silu_gate(yv, zz, p.dt_z);
+      p.y[r * p.D + c] = yv;
       if constexpr (RANK1) p.beta_out[r * (p.D + N) + c] = fmul(dt, uu);
     }
     if constexpr (RANK1) {

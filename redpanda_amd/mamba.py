@@ -145,6 +145,29 @@ class Mamba3Block(nn.Module):
     def _track_or_none(self):
         return self._track_gate() if self.config.n_track_state > 0 else None
 
+    def _gate_params(self):
+        """The parameters the gates are computed from."""
+        ps = [getattr(self, n) for n in ("A_log_mag", "A_phase", "A_log", "track_theta")
+              if hasattr(self, n)]
+        return ps
+
+    def _gates(self, record_grad):
+        """(A_real, A_imag, track).  Without an autograd graph to record they
+        are computed once and reused until a gate parameter changes (its
+        storage or its version counter, which every in-place update such as
+        an optimizer step or load_state_dict advances): an inference loop of
+        step() calls then skips five small kernels per layer."""
+        if record_grad:
+            return (*self._compute_A(), self._track_or_none())
+        key = tuple((t.data_ptr(), t._version, t.device) for t in self._gate_params())
+        hit = self.__dict__.get("_gate_cache")
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        with torch.no_grad():
+            val = (*self._compute_A(), self._track_or_none())
+        self.__dict__["_gate_cache"] = (key, val)
+        return val
+
     # ── projections (engine/mamba.py:284-301) ──
 
     def _ssm_proj(self, u):
@@ -260,11 +283,10 @@ class Mamba3Block(nn.Module):
         x_branch, z = self.in_proj(x_t).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
         x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
-        A_real, A_imag = self._compute_A()
-        track = self._track_or_none()
         grad = torch.is_grad_enabled() and (
             any(p.requires_grad for p in self.parameters()) or x_t.requires_grad or
             (state is not None and any(s.requires_grad for s in state)))
+        A_real, A_imag, track = self._gates(grad)
         rank1 = is_compact(state[1]) if state is not None else bool(compact)
         if grad:
             # differentiable: a length-1 scan from the cached state (a rank-1
@@ -278,11 +300,12 @@ class Mamba3Block(nn.Module):
             y = y.squeeze(1) + x_branch * self.D
             if rank1:
                 beta = self._compact_beta(x_dt, x_branch, Bc)
+            y = y * F.silu(z)
         else:
+            # the gate y * silu(z) is applied by the step kernel
             y, (h, beta) = hip_step(x_dt, x_branch, Bc, Cc, A_real, A_imag, track, self.D,
-                                    state, delta_softplus=True, compact=rank1)
-        out = self.out_proj(y * F.silu(z))
-        return out, (h, beta)
+                                    state, delta_softplus=True, compact=rank1, z=z)
+        return self.out_proj(y), (h, beta)
 
 
 class Mamba(nn.Module):

@@ -67,7 +67,7 @@ def _state_pair(h, b, R, D, N):
 
 
 def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None,
-             delta_softplus=False, compact=False):
+             delta_softplus=False, compact=False, z=None):
     """One step for R rollouts.
 
     delta, u: (R, D); Bc, Cc: (R, N) (contracted over p); A_real/A_imag:
@@ -77,6 +77,8 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     delta_softplus, `delta` is the dt projection x and the step uses
     F.softplus(x) (engine/mamba.py:300).  beta in rank-1 rows (R, D + N)
     returns rank-1 rows; with no state, `compact` chooses the form returned.
+    With the gate branch z (R, D) given, y is returned gated: y * silu(z)
+    (silu rounded to z's dtype, as torch computes it).
     """
     lib = _lib.load()
     R, D = u.shape
@@ -118,5 +120,15 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     a.broadcast_state = broadcast
     a.delta_softplus = 1 if delta_softplus else 0
     a.beta_rank1 = 1 if rank1 else 0
+    if z is not None:
+        if z.shape != (R, D) or not z.is_cuda:
+            raise ValueError(f"step: z must be a (R, D) = {(R, D)} device tensor")
+        if z.stride(-1) != 1:
+            z = z.contiguous()
+        a.z, a.z_sr = z.data_ptr(), z.stride(0)
+        try:
+            a.dtype_z = _lib.DTYPE_CODES[z.dtype]
+        except KeyError:
+            raise TypeError(f"step: unsupported dtype {z.dtype} for z") from None
     _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
     return y, (h_out, beta_out)

@@ -170,6 +170,15 @@ def test_step_rank1_rules(lib):
     assert lib.rp_step_check(ctypes.byref(_step_args(**{**bc, "beta_out": 0x200000 + (D + N) * 4}))) == 0
 
 
+def test_step_gate_rules(lib):
+    ok = dict(z=0x500000, z_sr=2 * 64, dtype_z=_lib.RP_BF16)
+    assert lib.rp_step_check(ctypes.byref(_step_args(**ok))) == 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "dtype_z": 9}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "z_sr": 63}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(**{**ok, "z": 0x500001}))) < 0
+    assert lib.rp_step_check(ctypes.byref(_step_args(reserved2=1))) < 0
+
+
 def test_initial_state_rules(lib):
     f = 0x10000
     assert lib.rp_scan_check(ctypes.byref(_good_args(h0=f, beta0=f))) == 0

@@ -143,3 +143,23 @@ def test_training_through_compact_step(gpu_lib):
     for k in g0:
         d = (g0[k] - g1[k]).abs().max() / (g0[k].abs().max() + 1e-30)
         assert float(d) <= 1e-6, k
+
+
+@pytest.mark.parametrize("zdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("R,D,NR,NT", SHAPES)
+def test_gated_step_equals_torch_gate(gpu_lib, R, D, NR, NT, zdt):
+    """y * silu(z) applied by the step kernel (z a strided chunk, fp32 or
+    bf16) is the same bits as torch's gate on the kernel's y, for both beta
+    forms."""
+    N = NR + NT
+    ins = _inputs(R, D, NR, NT, seed=R * 3 + D)
+    g = torch.Generator(device=dev).manual_seed(8)
+    xz = (torch.randn(R, 2 * D, device=dev, generator=g) * 3).to(zdt)
+    z = xz.chunk(2, dim=-1)[1]
+    h, bp, bfull = _rank1_state(R, D, N, seed=4)
+    for st in ((h, bfull), (h, bp)):
+        yg, (hg, bg) = hip_step(*ins, state=st, z=z)
+        y0, (h0, b0) = hip_step(*ins, state=st)
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y0 * F.silu(z)), st[1].dim()
+        assert torch.equal(hg, h0) and torch.equal(bg, b0)
