@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 7
+#define RP_ABI_VERSION 8
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -270,6 +270,33 @@ int rp_bcnorm_fwd(const rp_bcnorm_args* a, void* stream);
 
 /* The autograd of those ops in one pass (plus a small dw reduction). */
 int rp_bcnorm_bwd(const rp_bcnorm_args* a, const rp_bcnorm_grad* g, void* stream);
+
+/*
+ * Residual add + RMSNorm of the batched step's residual stream
+ * (engine/mamba.py:82-89, :592-597): x' = x + add (when add is given,
+ * written to x_out), out = (x' * rsqrt(mean(x'^2) + eps)) * w, per row.
+ * x: (rows, d) fp32 with row stride x_sr; add: NULL or (rows, d) in
+ * dtype_add with row stride add_sr; w: (d,) fp32; x_out, out: (rows, d)
+ * fp32 contiguous.  Forward only (inference); outputs must not overlap the
+ * inputs.
+ */
+typedef struct rp_rmsnorm_args {
+  int64_t rows, d;
+  int32_t dtype_add;
+  float eps;
+  const float* x;    int64_t x_sr;
+  const void* add;   int64_t add_sr;
+  const float* w;
+  float* x_out;
+  float* out;
+} rp_rmsnorm_args;
+
+/* Validate RMSNorm arguments on the host without launching anything. */
+int rp_rmsnorm_check(const rp_rmsnorm_args* a);
+
+/* The residual add and the next RMSNorm of Mamba.step's layer loop in one
+ * pass; replaces x + out and RMSNorm's five elementwise and reduction ops. */
+int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream);
 
 /* ABI version this library was built with (RP_ABI_VERSION). */
 int rp_abi_version(void);

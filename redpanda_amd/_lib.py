@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -94,6 +94,14 @@ class BcNormGrad(ctypes.Structure):
     ]
 
 
+class RmsNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", _i64), ("d", _i64), ("dtype_add", _i32), ("eps", ctypes.c_float),
+        ("x", _vp), ("x_sr", _i64), ("add", _vp), ("add_sr", _i64),
+        ("w", _vp), ("x_out", _vp), ("out", _vp),
+    ]
+
+
 # Every symbol include/redpanda_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "rp_abi_version": (ctypes.c_int, []),
@@ -109,6 +117,8 @@ SIGNATURES = {
     "rp_bcnorm_work_bytes": (_i64, [ctypes.POINTER(BcNormArgs)]),
     "rp_bcnorm_fwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), _vp]),
     "rp_bcnorm_bwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), ctypes.POINTER(BcNormGrad), _vp]),
+    "rp_rmsnorm_check": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs)]),
+    "rp_rmsnorm_fwd": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs), _vp]),
     "rp_mixer_out_check": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs)]),
     "rp_mixer_out_work_bytes": (_i64, [ctypes.POINTER(MixerOutArgs)]),
     "rp_mixer_out_fwd": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs), _vp]),

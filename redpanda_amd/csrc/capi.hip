@@ -797,4 +797,53 @@ int rp_bcnorm_bwd(const rp_bcnorm_args* a, const rp_bcnorm_grad* g, void* stream
   return RP_OK;
 }
 
+int rp_rmsnorm_check(const rp_rmsnorm_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "rmsnorm args: NULL");
+  if (a->rows < 0 || a->d < 0) return fail(RP_ERR_INVALID, "rmsnorm args: negative size");
+  if (a->d > kI32Max) return fail(RP_ERR_UNSUPPORTED, "rmsnorm args: d must fit in int32");
+  if (!(a->eps >= 0.f)) return fail(RP_ERR_INVALID, "rmsnorm args: eps must be >= 0");
+  if (a->rows * a->d == 0) return RP_OK;
+  if (!a->x || !a->w || !a->out) return fail(RP_ERR_INVALID, "rmsnorm args: NULL x / w / out");
+  if (a->x_sr < a->d) return fail(RP_ERR_INVALID, "rmsnorm args: x row stride shorter than d");
+  if (!aligned(a->x, 4) || !aligned(a->w, 4) || !aligned(a->out, 4))
+    return fail(RP_ERR_INVALID, "rmsnorm args: misaligned pointer");
+  const int64_t n = a->rows * a->d * 4;
+  const int64_t xb = ((a->rows - 1) * a->x_sr + a->d) * 4;
+  if (a->add != nullptr) {
+    if (a->dtype_add != RP_F32 && a->dtype_add != RP_BF16 && a->dtype_add != RP_F16)
+      return fail(RP_ERR_INVALID, "rmsnorm args: unknown dtype code %d", a->dtype_add);
+    if (a->add_sr < a->d || !aligned(a->add, elem_size(a->dtype_add)))
+      return fail(RP_ERR_INVALID, "rmsnorm args: add row stride shorter than d or misaligned");
+    if (!a->x_out || !aligned(a->x_out, 4))
+      return fail(RP_ERR_INVALID, "rmsnorm args: add needs a 4-byte aligned x_out");
+    const int64_t ab = ((a->rows - 1) * a->add_sr + a->d) * elem_size(a->dtype_add);
+    if (overlaps(a->x_out, n, a->x, xb) || overlaps(a->x_out, n, a->add, ab) ||
+        overlaps(a->x_out, n, a->out, n) || overlaps(a->out, n, a->add, ab))
+      return fail(RP_ERR_INVALID, "rmsnorm args: an output overlaps another buffer");
+  }
+  if (overlaps(a->out, n, a->x, xb))
+    return fail(RP_ERR_INVALID, "rmsnorm args: out overlaps x");
+  return RP_OK;
+}
+
+int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream) {
+  int st = rp_rmsnorm_check(a);
+  if (st != RP_OK) return st;
+  rp::RmsNormParams p{};
+  p.rows = a->rows;
+  p.d = (int)a->d;
+  p.dt_add = a->dtype_add;
+  p.eps = a->eps;
+  p.x = a->x;
+  p.xsr = a->x_sr;
+  p.add = a->add;
+  p.asr = a->add_sr;
+  p.w = a->w;
+  p.x_out = a->x_out;
+  p.out = a->out;
+  hipError_t e = rp::launch_rmsnorm_fwd(p, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "rmsnorm launch");
+  return RP_OK;
+}
+
 }  // extern "C"

@@ -159,6 +159,23 @@ constexpr int kBcNormWorkgroups = 1024;
 hipError_t launch_bcnorm_fwd(const BcNormParams& p, hipStream_t st);
 hipError_t launch_bcnorm_bwd(const BcNormParams& p, const BcNormGrad& g, hipStream_t st);
 
+// Residual add + RMSNorm of rows (forward only).
+struct RmsNormParams {
+  int64_t rows;
+  int d;
+  int dt_add;
+  float eps;
+  const float* x;   // (rows, d), row stride xsr
+  int64_t xsr;
+  const void* add;  // (rows, d) or null, row stride asr
+  int64_t asr;
+  const float* w;   // (d,)
+  float* x_out;     // (rows, d) contiguous: x + add (with add only)
+  float* out;       // (rows, d) contiguous
+};
+
+hipError_t launch_rmsnorm_fwd(const RmsNormParams& p, hipStream_t st);
+
 // Channels (one per thread) of the step tile kernel's workgroup, and the
 // most rollouts one of its workgroups walks.
 constexpr int kStepTile = kThreads;

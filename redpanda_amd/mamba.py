@@ -35,6 +35,7 @@ import torch.utils.checkpoint
 
 from redpanda_amd.bcnorm import hip_bcnorm_psum
 from redpanda_amd.mixer import hip_mixer_out
+from redpanda_amd.norm import hip_add_rmsnorm
 from redpanda_amd.scan import hip_scan_with_state, hip_trapezoidal_scan
 from redpanda_amd.step import compact_beta, full_beta, hip_step, is_compact
 
@@ -363,6 +364,24 @@ class Mamba(nn.Module):
         if cache is None:
             cache = [None] * len(self.layers)
         new_cache = []
+        record = torch.is_grad_enabled() and (
+            x.requires_grad or any(p.requires_grad for p in self.parameters()) or
+            any(t.requires_grad for st in cache if st is not None for t in st))
+        if not record and x.dtype == torch.float32 and x.dim() == 2 and len(self.layers) > 0:
+            # inference: each layer's residual add and the next RMSNorm (the
+            # next layer's, or norm_f) in one fused pass
+            _, xn = hip_add_rmsnorm(x, None, self.layers[0]["norm"].weight,
+                                    self.layers[0]["norm"].eps)
+            for i, layer in enumerate(self.layers):
+                out, st = layer["mixer"].step(xn, cache[i], compact=compact)
+                new_cache.append(st)
+                nxt = self.layers[i + 1]["norm"] if i + 1 < len(self.layers) else (
+                    self.norm_f if apply_final_norm else None)
+                if nxt is None:
+                    x = x + out
+                else:
+                    x, xn = hip_add_rmsnorm(x, out, nxt.weight, nxt.eps)
+            return (xn if apply_final_norm else x), new_cache
         for i, layer in enumerate(self.layers):
             out, st = layer["mixer"].step(layer["norm"](x), cache[i], compact=compact)
             x = x + out

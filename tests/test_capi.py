@@ -212,7 +212,8 @@ def _header_struct_fields(name):
                                           ("rp_mixer_out_args", "MixerOutArgs"),
                                           ("rp_mixer_out_grad", "MixerOutGrad"),
                                           ("rp_bcnorm_args", "BcNormArgs"),
-                                          ("rp_bcnorm_grad", "BcNormGrad")])
+                                          ("rp_bcnorm_grad", "BcNormGrad"),
+                                          ("rp_rmsnorm_args", "RmsNormArgs")])
 def test_ctypes_structs_mirror_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
     assert py == _header_struct_fields(cname)
@@ -335,3 +336,22 @@ def test_bcnorm_workspace(lib):
     g = _lib.BcNormGrad(dBc=0x4000000, dCc=0x4100000, dB_raw=0x5000000, dC_raw=0x5200000,
                         dwB=0x6000000, dwC=0x6001000, work=0x7000000, work_bytes=wb - 256)
     assert lib.rp_bcnorm_bwd(ctypes.byref(a), ctypes.byref(g), None) == -4
+
+
+def test_rmsnorm_check(lib):
+    def chk(**kw):
+        a = _lib.RmsNormArgs(rows=16, d=512, eps=1e-5, x=0x100000, x_sr=512, w=0x200000,
+                             out=0x300000)
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return lib.rp_rmsnorm_check(ctypes.byref(a))
+    assert chk() == 0
+    assert chk(x_sr=511) < 0
+    assert chk(eps=-1.0) < 0
+    assert chk(out=0x100000 + 64) < 0 and "overlaps" in lib.rp_last_error().decode()
+    add = dict(add=0x400000, add_sr=1024, dtype_add=_lib.RP_BF16, x_out=0x500000)
+    assert chk(**add) == 0
+    assert chk(**{**add, "x_out": None}) < 0
+    assert chk(**{**add, "dtype_add": 4}) < 0
+    assert chk(**{**add, "x_out": 0x400000}) < 0
+    assert chk(rows=0, x=None, w=None, out=None) == 0
