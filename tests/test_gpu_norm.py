@@ -24,7 +24,7 @@ def nrel(a, b):
 
 
 @pytest.mark.parametrize("dt", [None, torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("R,d", [(4096, 512), (7, 768), (33, 100), (5, 1), (0, 64)])
+@pytest.mark.parametrize("R,d", [(4096, 512), (7, 768), (33, 100), (5, 1), (0, 64), (3, 1500)])
 def test_add_rmsnorm_matches_torch(gpu_lib, R, d, dt):
     g = torch.Generator(device=dev).manual_seed(R + d)
     x = torch.randn(R, d, device=dev, generator=g) * 3
