@@ -1,0 +1,141 @@
+"""Seeded shape sweeps of the fused kernels around the scan and step against
+torch's ops (the reference's expressions) on the same GPU: odd sizes,
+strided and offset views, and every storage-dtype combination the C ABI
+accepts.  Each case is small; tolerances as in the per-kernel tests.
+"""
+
+import random
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from redpanda_amd.bcnorm import hip_bcnorm_psum
+from redpanda_amd.mixer import hip_mixer_out
+from redpanda_amd.norm import hip_add_rmsnorm
+from redpanda_amd.step import compact_beta, full_beta, hip_step
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+DTS = [torch.float32, torch.bfloat16, torch.float16]
+ULP = {torch.float32: 2.0 ** -23, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+
+
+def nrel(a, b):
+    a, b = a.float(), b.float()
+    return float((a - b).abs().max() / (b.abs().max() + 1e-30)) if b.numel() else 0.0
+
+
+def _view(shape, dt, g, pad, scale=1.0):
+    """A (..., D) view with `pad` extra leading elements per row."""
+    *lead, D = shape
+    base = (torch.randn(*lead, D + pad, device=dev, generator=g) * scale).to(dt)
+    return base[..., pad:]
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_mixer_sweep(gpu_lib, case):
+    rng = random.Random(100 + case)
+    g = torch.Generator(device=dev).manual_seed(case)
+    B, L, D = rng.randint(1, 4), rng.randint(1, 40), rng.choice([8, 64, 200, 264, 513, 1024])
+    du, dz, k = rng.choice(DTS), rng.choice(DTS), rng.choice([1, 2])
+    y = torch.randn(B, L, D, device=dev, generator=g)
+    u = _view((B, L, D), du, g, rng.choice([0, 8, 1]))
+    z = _view((B, L, D), dz, g, rng.choice([0, D, 3]), scale=3)
+    Dp = torch.randn(D, device=dev, generator=g)
+    a = [t.detach().clone().requires_grad_() if t.is_contiguous() else t.detach().requires_grad_()
+         for t in (y, u, z, Dp)]
+    out = hip_mixer_out(*a, k)
+    dout = torch.randn(B, L, D, device=dev, generator=g)
+    out.backward(dout)
+    r = [t.detach().clone().requires_grad_() for t in (y, u, z, Dp)]
+    yk = r[0] + r[1] * r[3]
+    if k == 2:
+        yk = yk + r[1] * r[3]
+    ref = yk * F.silu(r[2])
+    ref.backward(dout)
+    torch.cuda.synchronize()
+    tol = 4 * max(ULP[du], ULP[dz], 1e-6 / 4)
+    assert nrel(out, ref) <= tol
+    assert nrel(a[0].grad, r[0].grad) <= tol
+    assert nrel(a[1].grad, r[1].grad) <= 2 * tol
+    assert nrel(a[3].grad, r[3].grad) <= tol
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_bcnorm_sweep(gpu_lib, case):
+    rng = random.Random(200 + case)
+    g = torch.Generator(device=dev).manual_seed(case)
+    N, P = rng.randint(1, 128), rng.randint(1, 8)
+    T, dt, norm = rng.randint(0, 300), rng.choice(DTS), rng.random() < 0.8
+    K = N * P
+    x = (torch.randn(T, 3 + 2 * K, device=dev, generator=g) * 2).to(dt)
+    Bx, Cx = x[:, 3:3 + K], x[:, 3 + K:]
+    wB = 1 + 0.1 * torch.randn(K, device=dev, generator=g)
+    wC = 1 + 0.1 * torch.randn(K, device=dev, generator=g)
+    a = [Bx.detach().requires_grad_(), Cx.detach().requires_grad_(), wB.clone().requires_grad_(),
+         wC.clone().requires_grad_()]
+    Bc, Cc = hip_bcnorm_psum(*a, P, 1e-5, norm)
+    gB = torch.randn(T, N, device=dev, generator=g)
+    (Bc * gB + Cc).sum().backward()
+    r = [t.detach().float().requires_grad_() for t in (Bx, Cx)] + \
+        [t.clone().requires_grad_() for t in (wB, wC)]
+
+    def ref_norm(v, w):
+        if norm:
+            v = v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + 1e-5) * w
+        return v.view(T, N, P).sum(-1)
+
+    rB, rC = ref_norm(r[0], r[2]), ref_norm(r[1], r[3])
+    (rB * gB + rC).sum().backward()
+    torch.cuda.synchronize()
+    assert nrel(Bc, rB) <= 1e-6 and nrel(Cc, rC) <= 1e-6
+    tol = 4 * max(ULP[dt], 1e-6 / 4)
+    if T:
+        assert nrel(a[0].grad, r[0].grad) <= tol and nrel(a[1].grad, r[1].grad) <= tol
+        if norm:
+            assert nrel(a[2].grad, r[2].grad) <= 1e-5 and nrel(a[3].grad, r[3].grad) <= 1e-5
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_rmsnorm_sweep(gpu_lib, case):
+    rng = random.Random(300 + case)
+    g = torch.Generator(device=dev).manual_seed(case)
+    R, d = rng.randint(1, 500), rng.choice([1, 63, 64, 65, 257, 512, 1024, 1100])
+    x = _view((R, d), torch.float32, g, rng.choice([0, 5]), scale=2)
+    add = None if rng.random() < 0.3 else _view((R, d), rng.choice(DTS), g, rng.choice([0, 7]))
+    w = 1 + 0.1 * torch.randn(d, device=dev, generator=g)
+    xn, out = hip_add_rmsnorm(x, add, w, 1e-5)
+    xr = x if add is None else x + add
+    ref = xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-5) * w
+    torch.cuda.synchronize()
+    assert torch.equal(xn, xr) and nrel(out, ref) <= 1e-6
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_step_sweep(gpu_lib, case):
+    """Gated, softplus-on-load steps in both beta forms against the full-form
+    step and torch's gate, across kernel choices (d_state 4..72)."""
+    rng = random.Random(400 + case)
+    g = torch.Generator(device=dev).manual_seed(case)
+    NR, NT = rng.choice([(4, 0), (12, 4), (16, 4), (32, 8), (36, 4), (64, 8), (6, 2)])
+    N, R, D = NR + NT, rng.randint(1, 300), rng.choice([32, 100, 256, 300, 1024])
+    x = torch.randn(R, D, device=dev, generator=g) - 2
+    u = torch.randn(R, D, device=dev, generator=g)
+    Bc = torch.randn(R, N, device=dev, generator=g)
+    Cc = torch.randn(R, N, device=dev, generator=g)
+    Ar = -torch.exp(torch.rand(D, NR, device=dev, generator=g))
+    Ai = torch.rand(D, NR, device=dev, generator=g) * 3
+    Tk = torch.tanh(torch.randn(D, NT, device=dev, generator=g)) if NT else None
+    Dk = torch.randn(D, device=dev, generator=g)
+    zdt = rng.choice(DTS)
+    z = _view((R, D), zdt, g, rng.choice([0, D]), scale=3)
+    h = torch.randn(R, D, N, device=dev, generator=g)
+    bp = compact_beta(torch.rand(R, D, device=dev, generator=g) * 0.3,
+                      torch.randn(R, N, device=dev, generator=g))
+    st_full = (h, full_beta(bp, D).contiguous())
+    y0, (h0, b0) = hip_step(x, u, Bc, Cc, Ar, Ai, Tk, Dk, st_full, delta_softplus=True)
+    y1, (h1, b1) = hip_step(x, u, Bc, Cc, Ar, Ai, Tk, Dk, (h, bp), delta_softplus=True, z=z)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h0) and torch.equal(full_beta(b1, D), b0)
+    assert torch.equal(y1, y0 * F.silu(z))
