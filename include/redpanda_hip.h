@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 8
+#define RP_ABI_VERSION 9
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -173,30 +173,32 @@ typedef struct rp_step_args {
  * layer, 2 for a bidirectional one (the skip is added once per direction).
  * y: (B, L, D) fp32 contiguous (the scan output); u, z: (B, L, D) with batch
  * and time strides, inner stride 1, each RP_F32 / RP_BF16 / RP_F16; Dskip:
- * (D,) fp32; out: (B, L, D) fp32 contiguous (may be y itself; unused, and
- * may be NULL, for the backward).  silu(z) is rounded to z's
- * dtype before the product, as torch's ops on those dtypes do.
+ * (D,) fp32; out: (B, L, D) contiguous in dtype_out (may be y itself when
+ * fp32; unused, and may be NULL, for the backward).  silu(z) is rounded to
+ * z's dtype before the product, as torch's ops on those dtypes do; a 16-bit
+ * dtype_out rounds the fp32 result as the autocast cast before out_proj
+ * does.
  */
 typedef struct rp_mixer_out_args {
   int64_t B, L, D;
   int32_t k_skip;          /* 1 or 2 */
   int32_t dtype_u, dtype_z;
-  int32_t reserved;        /* must be 0 */
+  int32_t dtype_out;       /* of out and the backward's dout (RP_F32 = 0 by default) */
   const float* y;
   const void* u;  int64_t u_sb, u_sl;
   const void* z;  int64_t z_sb, z_sl;
   const float* Dskip;
-  float* out;
+  void* out;
 } rp_mixer_out_args;
 
 /*
- * Its backward given dout (B, L, D) fp32 contiguous: dy (fp32, the scan's
+ * Its backward given dout (B, L, D) contiguous in dtype_out: dy (fp32, the scan's
  * upstream gradient), du (u's dtype, the skip's share only), dz (z's dtype),
  * all (B, L, D) contiguous; dD (D,) fp32 (deterministic sums).  work:
  * rp_mixer_out_work_bytes() of scratch.
  */
 typedef struct rp_mixer_out_grad {
-  const float* dout;
+  const void* dout;        /* in dtype_out */
   float* dy;
   void* du;
   void* dz;

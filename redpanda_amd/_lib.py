@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -65,7 +65,7 @@ class StepArgs(ctypes.Structure):
 class MixerOutArgs(ctypes.Structure):
     _fields_ = [
         ("B", _i64), ("L", _i64), ("D", _i64),
-        ("k_skip", _i32), ("dtype_u", _i32), ("dtype_z", _i32), ("reserved", _i32),
+        ("k_skip", _i32), ("dtype_u", _i32), ("dtype_z", _i32), ("dtype_out", _i32),
         ("y", _vp), ("u", _vp), ("u_sb", _i64), ("u_sl", _i64),
         ("z", _vp), ("z_sb", _i64), ("z_sl", _i64), ("Dskip", _vp), ("out", _vp),
     ]

@@ -548,6 +548,7 @@ rp::MixerOutParams mixer_params(const rp_mixer_out_args* a, const MixPlan& m) {
   p.zsl = a->z_sl;
   p.Dskip = a->Dskip;
   p.out = a->out;
+  p.dt_out = a->dtype_out;
   p.rows_per_unit = m.rows_per_unit;
   p.units = m.units;
   p.vec = m.vec;
@@ -571,27 +572,27 @@ int rp_mixer_out_check(const rp_mixer_out_args* a) {
     return fail(RP_ERR_UNSUPPORTED, "mixer out args: B, L, D must each fit in int32");
   if (a->k_skip != 1 && a->k_skip != 2)
     return fail(RP_ERR_INVALID, "mixer out args: k_skip must be 1 or 2");
-  const int codes[2] = {a->dtype_u, a->dtype_z};
+  const int codes[3] = {a->dtype_u, a->dtype_z, a->dtype_out};
   for (int code : codes)
     if (code != RP_F32 && code != RP_BF16 && code != RP_F16)
       return fail(RP_ERR_INVALID, "mixer out args: unknown dtype code %d", code);
-  if (a->reserved != 0) return fail(RP_ERR_INVALID, "mixer out args: reserved field must be 0");
   if (a->B * a->L == 0 || a->D == 0) return RP_OK;
   if (!a->y || !a->u || !a->z || !a->Dskip)
     return fail(RP_ERR_INVALID, "mixer out args: NULL y/u/z/Dskip");
-  if (!aligned(a->y, 4) || !aligned(a->Dskip, 4) || !aligned(a->out, 4) ||
+  if (!aligned(a->y, 4) || !aligned(a->Dskip, 4) || !aligned(a->out, elem_size(a->dtype_out)) ||
       !aligned(a->u, elem_size(a->dtype_u)) || !aligned(a->z, elem_size(a->dtype_z)))
     return fail(RP_ERR_INVALID, "mixer out args: misaligned pointer");
   if (a->u_sb < 0 || a->u_sl < 0 || a->z_sb < 0 || a->z_sl < 0)
     return fail(RP_ERR_INVALID, "mixer out args: negative stride");
   // out is written once per element after that element's inputs are read:
-  // it may be y itself, but must not overlap u or z
+  // it may be y itself (fp32), but must not overlap u or z
   if (a->out == nullptr) return RP_OK;  // the backward reads no out
   const int64_t dense = a->B * a->L * a->D * 4;
-  if (overlaps(a->out, dense, a->u, span_bytes(a, a->u_sb, a->u_sl, elem_size(a->dtype_u))) ||
-      overlaps(a->out, dense, a->z, span_bytes(a, a->z_sb, a->z_sl, elem_size(a->dtype_z))))
+  const int64_t out_b = a->B * a->L * a->D * elem_size(a->dtype_out);
+  if (overlaps(a->out, out_b, a->u, span_bytes(a, a->u_sb, a->u_sl, elem_size(a->dtype_u))) ||
+      overlaps(a->out, out_b, a->z, span_bytes(a, a->z_sb, a->z_sl, elem_size(a->dtype_z))))
     return fail(RP_ERR_INVALID, "mixer out args: out overlaps u or z");
-  if (a->out != a->y && overlaps(a->out, dense, a->y, dense))
+  if (!(a->out == a->y && a->dtype_out == RP_F32) && overlaps(a->out, out_b, a->y, dense))
     return fail(RP_ERR_INVALID, "mixer out args: out partly overlaps y");
   return RP_OK;
 }
@@ -633,7 +634,8 @@ int rp_mixer_out_bwd(const rp_mixer_out_args* a, const rp_mixer_out_grad* g, voi
   }
   if (!g->dout || !g->dy || !g->du || !g->dz)
     return fail(RP_ERR_INVALID, "mixer out grad: NULL dout/dy/du/dz");
-  if (!aligned(g->dout, 4) || !aligned(g->dy, 4) || !aligned(g->du, elem_size(a->dtype_u)) ||
+  if (!aligned(g->dout, elem_size(a->dtype_out)) || !aligned(g->dy, 4) ||
+      !aligned(g->du, elem_size(a->dtype_u)) ||
       !aligned(g->dz, elem_size(a->dtype_z)))
     return fail(RP_ERR_INVALID, "mixer out grad: misaligned pointer");
   const int64_t n = a->B * a->L * a->D;
@@ -644,13 +646,13 @@ int rp_mixer_out_bwd(const rp_mixer_out_args* a, const rp_mixer_out_grad* g, voi
   const Span outs[4] = {{g->dy, n * 4}, {g->du, n * elem_size(a->dtype_u)},
                         {g->dz, n * elem_size(a->dtype_z)}, {g->dD, a->D * 4}};
   const Span ins[5] = {{a->y, n * 4}, {a->u, ubytes}, {a->z, zbytes}, {a->Dskip, a->D * 4},
-                       {g->dout, n * 4}};
+                       {g->dout, n * elem_size(a->dtype_out)}};
   for (int i = 0; i < 4; ++i) {
     for (int j = i + 1; j < 4; ++j)
       if (overlaps(outs[i].p, outs[i].n, outs[j].p, outs[j].n))
         return fail(RP_ERR_INVALID, "mixer out grad: outputs overlap");
     for (int j = 0; j < 5; ++j) {
-      if (i == 0 && j == 4 && g->dy == g->dout) continue;
+      if (i == 0 && j == 4 && g->dy == g->dout && a->dtype_out == RP_F32) continue;
       if (overlaps(outs[i].p, outs[i].n, ins[j].p, ins[j].n))
         return fail(RP_ERR_INVALID, "mixer out grad: an output overlaps an input");
     }

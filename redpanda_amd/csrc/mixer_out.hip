@@ -7,7 +7,9 @@
 //
 // Rounding follows torch's own ops in order, so fp32 inputs reproduce the
 // eager result: y + u*D (+ u*D), silu(z) = z / (1 + exp(-z)) rounded to z's
-// dtype, then the product in fp32.  Backward (autograd of the same graph):
+// dtype, then the product in fp32 -- stored in fp32, or rounded to the
+// autocast dtype the next projection casts it to (its gradient then arrives
+// in that dtype too).  Backward (autograd of the same graph):
 //     s = silu(z) (rounded),   dyk = dout * s,   ds = round_z(dout * yk)
 //     dz = round_z(ds * sig (1 + z (1 - sig))),  sig = 1 / (1 + exp(-z))
 //     dy = dyk (the scan's upstream gradient)
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void mixer_out_fwd_kernel(MixerOutParams 
     float yk = p.y[r * p.D + c] + u * dk;
     if (p.k_skip == 2) yk = yk + u * dk;
     const float s = round_to(z / (1.f + expf(-z)), p.dt_z);
-    p.out[r * p.D + c] = yk * s;
+    store_as(p.out, r * p.D + c, yk * s, p.dt_out);
   }
 }
 
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void mixer_out_bwd_kernel(MixerOutParams 
     const float z = load_in(p.z, cur.at(p.zsb, p.zsl) + c, p.dt_z);
     cur.next(p.L);
     const int64_t i = r * p.D + c;
-    const float dout = g.dout[i];
+    const float dout = load_in(g.dout, i, p.dt_out);
     float yk = p.y[i] + u * dk;
     if (p.k_skip == 2) yk = yk + u * dk;
     const float e = expf(-z);
@@ -161,6 +163,25 @@ __device__ __forceinline__ void store8(void* p, int64_t i, const float (&v)[kMix
   }
 }
 
+// The same for a dtype known only at run time (uniform across the launch).
+__device__ __forceinline__ void load8_rt(const void* p, int64_t i, float (&v)[kMixVec], int dt) {
+  if (dt == RP_F32)
+    load8<RP_F32>(p, i, v);
+  else if (dt == RP_BF16)
+    load8<RP_BF16>(p, i, v);
+  else
+    load8<RP_F16>(p, i, v);
+}
+
+__device__ __forceinline__ void store8_rt(void* p, int64_t i, const float (&v)[kMixVec], int dt) {
+  if (dt == RP_F32)
+    store8<RP_F32>(p, i, v);
+  else if (dt == RP_BF16)
+    store8<RP_BF16>(p, i, v);
+  else
+    store8<RP_F16>(p, i, v);
+}
+
 // Lane's first channel and its wave's rows: a workgroup takes row group
 // blockIdx.y (rows_per_unit rows) of one 512-channel tile, each wave a
 // quarter of the group.  False when the lane has no channels; the row range
@@ -199,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void mixer_out_fwd_vec_kernel(MixerOutPar
       const float s = round_to(z[k] / (1.f + expf(-z[k])), DZ);
       o[k] = yk * s;
     }
-    store8<RP_F32>(p.out, r * p.D + c0, o);
+    store8_rt(p.out, r * p.D + c0, o, p.dt_out);
   }
 }
 
@@ -225,7 +246,7 @@ __global__ __launch_bounds__(kThreads) void mixer_out_bwd_vec_kernel(MixerOutPar
     load8<DZ>(p.z, cur.at(p.zsb, p.zsl) + c0, z);
     const int64_t i = r * p.D + c0;
     load8f(p.y, i, y);
-    load8f(g.dout, i, dout);
+    load8_rt(g.dout, i, dout, p.dt_out);
     cur.next(p.L);
     float dy[kMixVec], du[kMixVec], dz[kMixVec];
 #pragma unroll

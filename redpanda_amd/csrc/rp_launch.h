@@ -104,14 +104,15 @@ struct MixerOutParams {
   const void* z;
   int64_t zsb, zsl;
   const float* Dskip;      // (D,)
-  float* out;              // (rows, D) fp32
+  void* out;               // (rows, D) in dt_out
+  int dt_out;              // dtype of out (and of the backward's dout)
   int64_t rows_per_unit;
   int units;
   int vec;                 // 1: 16-byte vectors of 8 channels per lane
 };
 
 struct MixerOutGrad {
-  const float* dout;  // (rows, D) fp32
+  const void* dout;   // (rows, D) in dt_out
   float* dy;          // (rows, D) fp32
   void* du;           // (rows, D) in u's dtype
   void* dz;           // (rows, D) in z's dtype

@@ -87,6 +87,15 @@ class RMSNorm(nn.Module):
         return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + self.eps) * self.weight
 
 
+def _gate_out_dtype():
+    """The dtype out_proj will read the gate's output in: autocast's when it
+    is on for the device, so the gate writes it directly (the same rounding
+    as the cast autocast would insert), else fp32 as the reference's op."""
+    if torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return torch.float32
+
+
 def _need_device(t, what):
     if not t.is_cuda:
         raise RuntimeError(
@@ -247,7 +256,8 @@ class Mamba3Block(nn.Module):
         bi = self.config.bidirectional
         y = self._scan_core(x_branch, x_dt, A_real, A_imag, Bc, Cc, bidirectional=bi,
                             contracted=True, delta_softplus=True)
-        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 2 if bi else 1))
+        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 2 if bi else 1,
+                                           out_dtype=_gate_out_dtype()))
 
     def forward_with_state(self, x, compact=False):
         """engine/mamba.py:269-282: output plus the final (h, beta) cache.
@@ -262,7 +272,8 @@ class Mamba3Block(nn.Module):
                                        contracted=True, delta_softplus=True)
         if compact:
             beta = self._compact_beta(x_dt[:, -1], x_branch[:, -1], Bc[:, -1])
-        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1)), (h, beta)
+        return self.out_proj(hip_mixer_out(y, x_branch, z, self.D, 1,
+                                           out_dtype=_gate_out_dtype())), (h, beta)
 
     @staticmethod
     def _compact_beta(x_dt, u, Bc):

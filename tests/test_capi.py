@@ -256,7 +256,9 @@ def test_mixer_out_check(lib):
     assert chk(out=0x1000000) == 0  # in place over y
     assert chk(k_skip=3) < 0 and "k_skip" in lib.rp_last_error().decode()
     assert chk(dtype_z=7) < 0
-    assert chk(reserved=1) < 0
+    assert chk(dtype_out=7) < 0
+    assert chk(dtype_out=_lib.RP_BF16) == 0
+    assert chk(dtype_out=_lib.RP_BF16, out=0x1000000) < 0  # a 16-bit out over fp32 y
     assert chk(z=None) < 0
     assert chk(out=None) == 0  # the backward's arguments carry no out
     assert lib.rp_mixer_out_fwd(ctypes.byref(_mixer_args(out=None)), None) < 0

@@ -227,3 +227,23 @@ def test_block_forward_uses_fused_gate(gpu_lib):
         for k, p in blk.named_parameters():
             d = (g_fused[k] - p.grad).abs().max() / (p.grad.abs().max() + 1e-30)
             assert float(d) <= 1e-5, f"grad {k} bi={bi}: {float(d):.2e}"
+
+
+@pytest.mark.parametrize("odt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [512, 300])
+def test_autocast_dtype_output(gpu_lib, odt, D):
+    """Output in out_proj's autocast dtype: the same bits as torch's fp32
+    result cast to it; its (16-bit) gradient gives the same gradients as the
+    fp32 output with that gradient upcast, as autocast's cast backward does."""
+    y, u, z, Dp = _inputs(3, 21, D, torch.bfloat16, seed=D)
+    a16 = [t.clone().requires_grad_() for t in (y, u, z, Dp)]
+    out16 = hip_mixer_out(*a16, 2, out_dtype=odt)
+    ref = eager(y, u, z, Dp, 2)
+    assert out16.dtype == odt and torch.equal(out16, ref.to(odt))
+    g = torch.randn(3, 21, D, device=dev).to(odt)
+    out16.backward(g)
+    a32 = [t.clone().requires_grad_() for t in (y, u, z, Dp)]
+    hip_mixer_out(*a32, 2).backward(g.float())
+    torch.cuda.synchronize()
+    for p16, p32 in zip(a16, a32):
+        assert torch.equal(p16.grad, p32.grad)
