@@ -24,8 +24,9 @@
 // (a bias below 0.01 ulp).  (Rounding Ar*log2(e) and 256*Ai/(2 pi) once per
 // state is harmless by contrast: its error scales with dt*A, so it stays
 // ~1 ulp of the state over any memory length.)
-// The forward, the step and the backward's recompute share the code, so the
-// backward recomputes exactly the gates the forward used.
+// The forward and the step share the gate code (cos from a per-index cubic
+// record), so the step continues the scan bit for bit; the backward
+// evaluates the same cubic from (cos, sin) pairs, to within an ulp.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -104,10 +105,14 @@ __device__ __forceinline__ float ffma(float a, float b, float c) { return __buil
 // exp2 on the transcendental unit (v_exp_f32).
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// The cos / sin table (kTab entries of 2 pi k / kTab) copied into LDS once
-// per workgroup; read after the workgroup's next barrier.
-__device__ __forceinline__ void fill_sincos_table(float2* tab, int tid) {
-  for (int k = tid; k < kTab; k += kThreads) tab[k] = kSinCosTable[k];
+// The gate tables copied into LDS once per workgroup (read after the
+// workgroup's next barrier): the cos records (forward and step) or the
+// (cos, sin) pairs (backward) of the kTab table angles 2 pi k / kTab.
+__device__ __forceinline__ void fill_cos_records(float4* ctab, int tid) {
+  for (int k = tid; k < kTab; k += kThreads) ctab[k] = kCosRec[k];
+}
+__device__ __forceinline__ void fill_sincos_pairs(float2* cstab, int tid) {
+  for (int k = tid; k < kTab; k += kThreads) cstab[k] = kSinCos[k];
 }
 
 // Per-state gate parameters held in registers: pah = fl(A_real log2(e)) and
@@ -173,40 +178,72 @@ struct GateKind {
   static constexpr int kTJ = TJ;
 };
 
-// Rotational gate g = 2^(dt pah) cos(a dt wh), a = 2 pi / 256; with WITH_SIN
-// also es = 2^(dt pah) sin(a dt wh) for the backward.  The angle dt*wh is split
-// exactly into an integer k (the table index, by the round-to-integer
-// addition) and a remainder |r| <= 1/2.  The cos path is the same code in
-// both instantiations, so g is bitwise the same.
-//
-// The gate is split in two phases so that a caller can start the
-// exponentials and table reads of several states before finishing any of
-// them (rot_gate_issue, then rot_gate_finish); rot_gate is the two in a row.
+// Rotational gate g = 2^(dt pah) cos(a dt wh), a = 2 pi / 256.  The exact
+// product dt*wh (an FMA with the round-to-integer constant, then one with
+// -k) splits into an integer k, the table index, and a remainder |r| <= 1/2
+// rounded once.  The split needs |dt wh| < 2^22, i.e. |dt A_imag| < 1e5.
+// Returns the table index (low kTabBits of the rounded value).
+__device__ __forceinline__ int angle_split(float dt, float wh, float& r) {
+  const float t = ffma(dt, wh, kRint);
+  const float kf = t - kRint;  // rint(dt wh), exact
+  r = ffma(dt, wh, -kf);
+  return __float_as_int(t) & (kTab - 1);
+}
+
+// Two flavours of the same expansion, in two phases each so that a caller
+// can start the exponentials and table reads of several states before
+// finishing any of them (issue, then finish):
+//   * the forward and the step: cos from the index's cos record (one 16-byte
+//     table read, three FMAs);
+//   * the backward: cos and also es = 2^(dt pah) sin(a dt wh) from the
+//     index's (cos, sin) pair (one 8-byte read; the two expansions share r^2,
+//     cos - 1 and sin of the remainder).  Its gate is the forward's to
+//     within an ulp (the same cubic, rounded differently).
 struct GatePart {
   float e;    // 2^(dt pah)
   float r;    // angle remainder, |r| <= 1/2 (table steps)
+  float4 cr;  // cos record of the table angle
+};
+
+struct GatePartCS {
+  float e;
+  float r;
   float2 cs;  // cos, sin of the table angle
 };
 
 __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh, bool imag,
-                                                   const float2* tab) {
+                                                   const float4* ctab) {
   GatePart g;
+  g.e = exp2_hw(fmul(dt, pah));
+  if (!imag) {
+    g.r = 0.f;
+    g.cr = make_float4(1.f, 0.f, 0.f, 0.f);
+    return g;
+  }
+  g.cr = ctab[angle_split(dt, wh, g.r)];
+  return g;
+}
+
+__device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag) {
+  if (!imag) return g.e;
+  const float r = g.r;
+  return fmul(g.e, ffma(r, ffma(r, ffma(r, g.cr.w, g.cr.z), g.cr.y), g.cr.x));
+}
+
+__device__ __forceinline__ GatePartCS rot_gate_issue_cs(float dt, float pah, float wh, bool imag,
+                                                        const float2* cstab) {
+  GatePartCS g;
   g.e = exp2_hw(fmul(dt, pah));
   if (!imag) {
     g.r = 0.f;
     g.cs = make_float2(1.f, 0.f);
     return g;
   }
-  const float w = fmul(dt, wh);
-  const float t = w + kRint;
-  const float kf = t - kRint;  // rint(w), exact
-  g.r = w - kf;                // exact
-  g.cs = tab[__float_as_int(t) & (kTab - 1)];
+  g.cs = cstab[angle_split(dt, wh, g.r)];
   return g;
 }
 
-template <bool WITH_SIN>
-__device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag, float& es) {
+__device__ __forceinline__ float rot_gate_finish_cs(const GatePartCS& g, bool imag, float& es) {
   if (!imag) {
     es = 0.f;
     return g.e;
@@ -216,19 +253,9 @@ __device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag, f
   const float cm1 = fmul(r2, kC2);                 // cos - 1
   const float sx = fmul(r, ffma(r2, kS3, kS1));    // sin
   const float cv = ffma(-g.cs.y, sx, ffma(g.cs.x, cm1, g.cs.x));
-  if (WITH_SIN) {
-    const float sv = ffma(g.cs.x, sx, ffma(g.cs.y, cm1, g.cs.y));
-    es = fmul(g.e, sv);
-  } else {
-    es = 0.f;
-  }
+  const float sv = ffma(g.cs.x, sx, ffma(g.cs.y, cm1, g.cs.y));
+  es = fmul(g.e, sv);
   return fmul(g.e, cv);
-}
-
-template <bool WITH_SIN>
-__device__ __forceinline__ float rot_gate(float dt, float pah, float wh, bool imag,
-                                          const float2* tab, float& es) {
-  return rot_gate_finish<WITH_SIN>(rot_gate_issue(dt, pah, wh, imag, tab), imag, es);
 }
 
 // Whether state slot j of lane slice s is rotational (n = j*S + s < NR).
@@ -253,49 +280,43 @@ __device__ __forceinline__ bool imag_of(bool has_imag) {
   return GK::kImag == 2 ? has_imag : GK::kImag == 1;
 }
 
-// Gate of state slot j for lane slice s: rotational if n < NR, else the
-// tracking gate pah = tanh(theta) (pad states beyond N carry 0 and B = C = 0).
-template <int S, class GK, bool WITH_SIN>
+// Gate of state slot j for lane slice s (forward flavour): rotational if
+// n < NR, else the tracking gate pah = tanh(theta) (pad states beyond N
+// carry 0 and B = C = 0).
+template <int S, class GK>
 __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pah,
-                                         float wh, const float2* tab, float& es) {
-  if (j >= GK::kTJ) {
-    es = 0.f;
-    return pah;
-  }
-  if (j < GK::kRJ) return rot_gate<WITH_SIN>(dt, pah, wh, imag_of<GK>(has_imag), tab, es);
-  if (j * S >= NR) {
-    es = 0.f;
-    return pah;
-  }
-  const float gr = rot_gate<WITH_SIN>(dt, pah, wh, imag_of<GK>(has_imag), tab, es);
+                                         float wh, const float4* ctab) {
+  if (j >= GK::kTJ) return pah;
+  const bool imag = imag_of<GK>(has_imag);
+  if (j < GK::kRJ) return rot_gate_finish(rot_gate_issue(dt, pah, wh, imag, ctab), imag);
+  if (j * S >= NR) return pah;
+  const float gr = rot_gate_finish(rot_gate_issue(dt, pah, wh, imag, ctab), imag);
   if ((j + 1) * S <= NR || j * S + s < NR) return gr;
-  es = 0.f;
   return pah;
 }
 
-// gate_of in two phases (see rot_gate_issue): gate_issue starts the
-// rotational part of slot j, gate_finish returns the gate; the pair computes
-// exactly gate_of.
+// The backward flavour of gate_of (with es), in two phases: gate_issue_cs
+// starts the rotational part of slot j, gate_finish_cs returns the gate.
 template <int S, class GK>
-__device__ __forceinline__ GatePart gate_issue(int j, int NR, bool has_imag, float dt, float pah,
-                                               float wh, const float2* tab) {
-  if (j >= GK::kTJ || (j >= GK::kRJ && j * S >= NR)) return GatePart{0.f, 0.f, {1.f, 0.f}};
-  return rot_gate_issue(dt, pah, wh, imag_of<GK>(has_imag), tab);
+__device__ __forceinline__ GatePartCS gate_issue_cs(int j, int NR, bool has_imag, float dt,
+                                                    float pah, float wh, const float2* cstab) {
+  if (j >= GK::kTJ || (j >= GK::kRJ && j * S >= NR)) return GatePartCS{0.f, 0.f, {1.f, 0.f}};
+  return rot_gate_issue_cs(dt, pah, wh, imag_of<GK>(has_imag), cstab);
 }
 
-template <int S, class GK, bool WITH_SIN>
-__device__ __forceinline__ float gate_finish(int j, int s, int NR, bool has_imag,
-                                             const GatePart& part, float pah, float& es) {
+template <int S, class GK>
+__device__ __forceinline__ float gate_finish_cs(int j, int s, int NR, bool has_imag,
+                                                const GatePartCS& part, float pah, float& es) {
   if (j >= GK::kTJ) {
     es = 0.f;
     return pah;
   }
-  if (j < GK::kRJ) return rot_gate_finish<WITH_SIN>(part, imag_of<GK>(has_imag), es);
+  if (j < GK::kRJ) return rot_gate_finish_cs(part, imag_of<GK>(has_imag), es);
   if (j * S >= NR) {
     es = 0.f;
     return pah;
   }
-  const float gr = rot_gate_finish<WITH_SIN>(part, imag_of<GK>(has_imag), es);
+  const float gr = rot_gate_finish_cs(part, imag_of<GK>(has_imag), es);
   if ((j + 1) * S <= NR || j * S + s < NR) return gr;
   es = 0.f;
   return pah;
@@ -324,20 +345,45 @@ __device__ __forceinline__ void load_gate_regs(GateRegs<NPL>& gp, const float* A
 // previous step's hb.  Shared verbatim by the scan and step kernels.
 template <int S, int NPL, class GK>
 __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
-                                            const GateRegs<NPL>& gp, const float2* tab, float dt,
+                                            const GateRegs<NPL>& gp, const float4* ctab, float dt,
                                             float hdu, const float* __restrict__ Bs,
                                             const float* __restrict__ Cs, int s, int NR,
                                             bool has_imag) {
   float y = 0.f;
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
-    float unused;
-    const float g = gate_of<S, GK, false>(j, s, NR, has_imag, dt, gp.pah[j], gp.wh[j], tab, unused);
+    const float g = gate_of<S, GK>(j, s, NR, has_imag, dt, gp.pah[j], gp.wh[j], ctab);
     const float hb = fmul(hdu, Bs[j]);
     const float sm = h[j] + hbp[j];
     h[j] = ffma(g, sm, hb);
     hbp[j] = hb;
     y = ffma(h[j], Cs[j], y);
+  }
+  return y;
+}
+
+// fwd_update with the carried value sm_j = h_j + hb_j, the sum the next
+// step's gate multiplies, in place of the pair (h_j, hb_j): one register per
+// state across steps instead of two, and the same operations on the same
+// values, so the results are bitwise those of fwd_update.  The step's h_j and
+// hb_j are left in hn / hbn for a caller that stores them.
+template <int S, int NPL, class GK>
+__device__ __forceinline__ float fwd_update_carried(float (&sm)[NPL], float (&hn)[NPL],
+                                                    float (&hbn)[NPL], const GateRegs<NPL>& gp,
+                                                    const float4* ctab, float dt, float hdu,
+                                                    const float* __restrict__ Bs,
+                                                    const float* __restrict__ Cs, int s, int NR,
+                                                    bool has_imag) {
+  float y = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const float g = gate_of<S, GK>(j, s, NR, has_imag, dt, gp.pah[j], gp.wh[j], ctab);
+    const float hb = fmul(hdu, Bs[j]);
+    const float h = ffma(g, sm[j], hb);
+    y = ffma(h, Cs[j], y);
+    sm[j] = h + hb;
+    hn[j] = h;
+    hbn[j] = hb;
   }
   return y;
 }

@@ -17,9 +17,12 @@
 // directions.  The forward stored the state entering every kCkptK-step chunk;
 // the backward walks chunks in reverse, recomputes the chunk's K steps into
 // registers (keeping s_{t-1}, the gate and e*sin, so the adjoint evaluates
-// no transcendental), then runs the adjoint over them.  The recompute calls
-// the forward's gate code (with the sine added), so it rebuilds the forward's
-// states exactly.
+// no transcendental), then runs the adjoint over them.  The recompute
+// evaluates the forward's gate expansion from (cos, sin) table pairs, which
+// also gives the sine (an 8-byte table read, where the forward's 16-byte cos
+// record would double the LDS traffic of a kernel that already shares the
+// LDS with its reductions); each gate matches the forward's to within an ulp
+// and every chunk restarts from the forward's checkpoint.
 //
 // Streaming: the per-step inputs (dt, (dt*u)/2, u, dy per channel; B, C per
 // state) of a chunk and of the step before it sit in one of two LDS slots.
@@ -70,7 +73,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float sC[2][KS][NP];
   __shared__ __align__(16) float sRed[KR][2][NP][RWP];  // per-row channel sums of dB, dC
   __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
-  __shared__ float2 sTab[kTab];             // cos, sin of 2 pi k / kTab
+  __shared__ float2 sCS[kTab];              // (cos, sin) pairs of the gate table
   // per-thread float64 sums of the parameter gradients over the batch group
   // (dA_real or dtrack, dA_imag), kept in LDS to spare registers
   __shared__ double sPar[2][NPL][kThreads];
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 
   GateRegs<NPL> gp;  // loads issued first, so the table copy overlaps them
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
-  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
+  fill_sincos_pairs(sCS, tid);  // first read after the staging barrier below
   // pam: the coefficient of the ddt sum over rotational states, zero for a
   // tracking state (only read for slots whose kind is decided at run time)
   float pam[NPL];
@@ -305,15 +308,14 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               const float dt = sCh[SL][m + 1][cl].x;
               const float hd = sCh[SL][m + 1][cl].y;
               // start every state's exponential and table read, then finish
-              GatePart part[NPL];
+              GatePartCS part[NPL];
 #pragma unroll
               for (int j = 0; j < NPL; ++j)
-                part[j] = gate_issue<S, GK>(j, p.NR, has_imag, dt, gp.pah[j], gp.wh[j], sTab);
+                part[j] = gate_issue_cs<S, GK>(j, p.NR, has_imag, dt, gp.pah[j], gp.wh[j], sCS);
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
                 float es;
-                const float g =
-                    gate_finish<S, GK, true>(j, s, p.NR, has_imag, part[j], gp.pah[j], es);
+                const float g = gate_finish_cs<S, GK>(j, s, p.NR, has_imag, part[j], gp.pah[j], es);
                 const float hb = fmul(hd, sB[SL][m + 1][s * NPL + j]);
                 const float sm = hc[j] + hbp[j];
                 SP[m][j] = sm;

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
   __shared__ float sY[TB][CB];     // the block's y, written out channel-contiguous
-  __shared__ float2 sTab[kTab];      // cos, sin of 2 pi k / kTab
+  __shared__ float4 sCos[kTab];      // cos records of the gate table
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
@@ -43,20 +43,19 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
 
   GateRegs<NPL> gp;  // loads issued first, so the table copy overlaps them
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
-  fill_sincos_table(sTab, tid);  // first read after the staging barrier below
+  fill_cos_records(sCos, tid);  // first read after the staging barrier below
 
   const int nblk = (L + TB - 1) / TB;
   for (int dir = 0; dir < p.ndir; ++dir) {
-    float h[NPL], hbp[NPL];
+    // sm = h + hb of the previous step (of the initial state h0, beta0 / 2)
+    float sm[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const int n = j * S + s;
-      h[j] = 0.f;
-      hbp[j] = 0.f;
+      sm[j] = 0.f;
       if (dir == 0 && p.h0 != nullptr && cvalid && n < p.N) {
         const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
-        h[j] = p.h0[idx];
-        hbp[j] = 0.5f * p.beta0[idx];
+        sm[j] = p.h0[idx] + 0.5f * p.beta0[idx];
       }
     }
     // y of the block starting at step i0 (cnt steps) from sY: coalesced, and
@@ -114,34 +113,37 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
       __syncthreads();
       for (int r = 0; r < cnt; ++r) {
         const int i = i0 + r;
-        if (o.ckpt != nullptr && i > 0 && (i % kCkptK) == 0) {
-          // state entering chunk i/K, in a coalesced [tile][wave][j][lane] record
-          const int64_t rec = ((int64_t)(dir * p.B + b) * p.nck + (i / kCkptK - 1)) * p.ntiles + tile;
+        const float2 dh = sDH[r][cl];
+        float h[NPL], hb[NPL];
+        float y = fwd_update_carried<S, NPL, GK>(sm, h, hb, gp, sCos, dh.x, dh.y, &sB[r][s * NPL],
+                                                 &sC[r][s * NPL], s, p.NR, has_imag);
+        // the channel's S lanes hold the same total and store the same value
+        sY[r][cl] = reduce_states<S>(y);
+        if (o.ckpt != nullptr && ((i + 1) % kCkptK) == 0 && i + 1 < L) {
+          // state entering chunk (i+1)/K, in a coalesced [tile][wave][j][lane] record
+          const int64_t rec =
+              ((int64_t)(dir * p.B + b) * p.nck + ((i + 1) / kCkptK - 1)) * p.ntiles + tile;
           float* dst = o.ckpt + (rec * kWaves + wave) * (NPL * kWave) + lane;
 #pragma unroll
           for (int j = 0; j < NPL; ++j) dst[j * kWave] = h[j];
         }
-        const float2 dh = sDH[r][cl];
-        float y = fwd_update<S, NPL, GK>(h, hbp, gp, sTab, dh.x, dh.y, &sB[r][s * NPL],
-                                         &sC[r][s * NPL], s, p.NR, has_imag);
-        // the channel's S lanes hold the same total and store the same value
-        sY[r][cl] = reduce_states<S>(y);
+        if (dir == 0 && i == L - 1 && o.h_last != nullptr && cvalid) {
+          // the final state (h, beta) that step() continues from
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            const int n = j * S + s;
+            if (n < p.N) {
+              const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
+              o.h_last[idx] = h[j];
+              o.beta_last[idx] = 2.f * hb[j];
+            }
+          }
+        }
       }
     }
     if (nblk > 0) {
       __syncthreads();
       write_y((nblk - 1) * TB, L - (nblk - 1) * TB);
-    }
-    if (dir == 0 && o.h_last != nullptr && cvalid) {
-#pragma unroll
-      for (int j = 0; j < NPL; ++j) {
-        const int n = j * S + s;
-        if (n < p.N) {
-          const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
-          o.h_last[idx] = h[j];
-          o.beta_last[idx] = 2.f * hbp[j];
-        }
-      }
     }
   }
 }

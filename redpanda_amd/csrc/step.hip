@@ -44,8 +44,8 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   const bool cvalid = c < p.D;
   const bool has_imag = p.Ai != nullptr;
 
-  __shared__ float2 sTab[kTab];  // cos, sin of 2 pi k / kTab
-  fill_sincos_table(sTab, tid);
+  __shared__ float4 sCos[kTab];  // cos records of the gate table
+  fill_cos_records(sCos, tid);
   GateRegs<NPL> gp;
   float h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
   float dt = 0.f, uu = 0.f;
@@ -76,9 +76,9 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
     }
   }
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
-  __syncthreads();  // the sin/cos table
+  __syncthreads();  // the gate table
   const float hd = 0.5f * fmul(dt, uu);
-  float y = fwd_update<S, NPL, GK>(h, hbp, gp, sTab, dt, hd, Bs, Cs, s, p.NR, has_imag);
+  float y = fwd_update<S, NPL, GK>(h, hbp, gp, sCos, dt, hd, Bs, Cs, s, p.NR, has_imag);
   y = reduce_states<S>(y);
   if (cvalid) {
 #pragma unroll
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
   constexpr int TCH = kStepTile;
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
-  __shared__ float2 sTab[kTab];           // cos, sin of 2 pi k / kTab
+  __shared__ float4 sCos[kTab];           // cos records of the gate table
   __shared__ float sBC[kStepRiMax][NBC * NP];  // B, C (B_prev) rows of the workgroup's rollouts
   // the (h, beta) block of one rollout: TCH channels x NP states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NV
@@ -206,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
   for (int n = 0; n < NP; ++n) graw[n] = gate_param_load(p.Ar, p.Ai, p.Tk, cld, n, N, p.NR, p.NT, true);
   const float dsk = p.Dskip[cld];
-  fill_sincos_table(sTab, tid);
+  fill_cos_records(sCos, tid);
 #pragma unroll
   for (int k = 0; k < BCPT; ++k) {
     const int e = tid + k * kThreads;
@@ -283,8 +283,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
       // same bits as the product the full form stored
       const float hbp = RANK1 ? fmul(hdp, Bp[n]) : 0.5f * bs;
-      float unused;
-      const float g = gate_of<S, GK, false>(j, q, p.NR, has_imag, dt, pah[n], wh[n], sTab, unused);
+      const float g = gate_of<S, GK>(j, q, p.NR, has_imag, dt, pah[n], wh[n], sCos);
       const float hb = fmul(hd, Bs[n]);
       const float sm = hs + hbp;
       hs = ffma(g, sm, hb);
