@@ -38,8 +38,9 @@
 //   * over channels (dB, dC): DPP row rotations inside each 16-lane row, the
 //     row partials staged in LDS, then a balanced 16-way sum per output, per tile;
 //     the per-tile partials are summed in float64 by a second kernel;
-//   * parameter gradients (dA, dTk): K-step fp32 chunk sums accumulated in
-//     float64 per lane over the batch group, then float64 across groups.
+//   * parameter gradients (dA, dTk): fp32 sums over up to 16 chunks (64
+//     steps) accumulated in float64 per lane over the batch group, then
+//     float64 across groups.
 
 #include <type_traits>
 
@@ -47,6 +48,10 @@
 #include "rp_launch.h"
 
 namespace rp {
+
+// Chunks whose parameter-gradient terms are summed in fp32 before they are
+// added into the float64 sums (64 steps).
+constexpr int kParChunks = 16;
 
 template <int S, int NPL, class GK>
 __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
@@ -230,6 +235,17 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           if (io.dbeta_last != nullptr) gr[j] = 2.f * io.dbeta_last[idx];
         }
       }
+      // parameter-gradient sums over up to kParChunks chunks (fp32), added
+      // into the float64 per-thread sums every kParChunks chunks and at the
+      // end of the sweep; cpt: the tracking-state sum of a slot decided at
+      // run time
+      float cpa[NPL], cpb[NPL], cpt[NPL];
+#pragma unroll
+      for (int j = 0; j < NPL; ++j) {
+        cpa[j] = 0.f;
+        cpb[j] = 0.f;
+        cpt[j] = 0.f;
+      }
       // the entry state of the next chunk to process, loaded one chunk ahead
       float hnx[NPL];
       if (nct > 0) {
@@ -329,14 +345,6 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           }
           // adjoint over the chunk, last step first.  Parameter gradients
           // sum into chunk-local fp32 accumulators, then into float64.
-          // cpt: the tracking-state sum of a slot decided at run time
-          float cpa[NPL], cpb[NPL], cpt[NPL];
-#pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            cpa[j] = 0.f;
-            cpb[j] = 0.f;
-            cpt[j] = 0.f;
-          }
 #pragma unroll
           for (int m = K - 1; m >= 0; --m) {
             if (FULL || m < kcnt) {
@@ -428,12 +436,17 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               __syncthreads();
             }
           }
+          if (ch % kParChunks == 0) {
 #pragma unroll
-          for (int j = 0; j < NPL; ++j) {
-            const float a = (j >= GK::kRJ && j < GK::kTJ && !is_rot<S, GK>(j, s, p.NR)) ? cpt[j]
-                                                                                        : cpa[j];
-            sPar[0][j][tid] += (double)a;
-            if (j < GK::kTJ) sPar[1][j][tid] += (double)cpb[j];
+            for (int j = 0; j < NPL; ++j) {
+              const float a = (j >= GK::kRJ && j < GK::kTJ && !is_rot<S, GK>(j, s, p.NR)) ? cpt[j]
+                                                                                          : cpa[j];
+              sPar[0][j][tid] += (double)a;
+              if (j < GK::kTJ) sPar[1][j][tid] += (double)cpb[j];
+              cpa[j] = 0.f;
+              cpb[j] = 0.f;
+              cpt[j] = 0.f;
+            }
           }
         };
         if (kcnt == K) {
