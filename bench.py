@@ -24,6 +24,9 @@ Besides the headline number the JSON line carries:
                 beside the reference's layer with only its scan swapped;
   mixer_gate    the fused (y + 2 u D) silu(z) gate after the scan: kernel
                 durations and bytes, and fwd + bwd against torch's ops;
+  rollout_boundary  one ply's host transfers for 4096 rollouts through the
+                pinned boundary (one upload, the top-k kernel, one download)
+                beside the reference's per-rollout reads, sampled;
   cpu_baseline  the reference's CPU PyTorch path (the oracle's fp32
                 restatement) on a bounded sample, on this host's cores.
 Only one GPU is used; --gpus above 1 exits with a message.
@@ -70,6 +73,7 @@ def parse():
                     help="skip the long-sequence (L=2048) scan line")
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer comparison")
     ap.add_argument("--no-mixer", action="store_true", help="skip the mixer-gate kernels")
+    ap.add_argument("--no-rollout", action="store_true", help="skip the rollout-boundary ply")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--profile-pass", action="store_true",
@@ -494,6 +498,87 @@ def bench_mixer(torch, args):
     fb, bb = mixer_bytes(y.numel())
     return dict(t_fwd=t_f, t_bwd=t_b, fwd_bytes=fb, bwd_bytes=bb, t_fused=t_fused,
                 t_torch=t_torch, t_fwd_warm=t_f_warm, t_bwd_warm=t_b_warm)
+
+
+# One ply of 4096 lockstep rollouts: the Search-Mamba continuation head's
+# logits over the 8192-token move vocabulary, the top-8 candidates the
+# policy-guided rollout walks (engine/mars_search.py:66, policy_top_k=8), and
+# about 40 legal moves per position for the fastchess path.
+ROLLOUT_SHAPE = dict(R=4096, V=8192, k=8, legal=40)
+
+
+def bench_rollout(torch, args, plies=20, sample=256):
+    """Host-inclusive time of one ply's transfers: redpanda_amd.rollout's
+    pinned boundary against the reference's pattern (a pageable token upload,
+    each rollout's continuation row read with .cpu() and its top-k taken in
+    numpy, the values read with .cpu().tolist()), the latter timed on
+    `sample` rollouts and scaled to R."""
+    import numpy as np
+    from redpanda_amd import _lib
+    from redpanda_amd.rollout import PlyBoundary
+    sh = ROLLOUT_SHAPE
+    R, V, k, M = sh["R"], sh["V"], sh["k"], sh["legal"]
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(11)
+    cont = torch.randn(R, V, device=dev, generator=g)
+    vals = torch.tanh(torch.randn(R, 1, device=dev, generator=g))
+    rng = np.random.default_rng(11)
+    tokens = rng.integers(0, V, R).tolist()
+    legal = rng.integers(0, V, (R, M))
+    pb = PlyBoundary(R, top_k=k, device=dev, max_legal=64)
+    out = torch.empty((R, 2 * k + 1), dtype=torch.float32, device=dev)
+    for _ in range(3):
+        pb.push_tokens(tokens)
+        pb.pull(vals, cont)
+        pb.pull_legal(cont, legal)
+    torch.cuda.synchronize()
+    # the kernel alone: prebuilt arguments, so the launches outpace the GPU
+    lib = _lib.load()
+    a = _lib.PlyTopkArgs(R=R, V=V, k=k, dtype_logits=_lib.RP_F32, logits=cont.data_ptr(),
+                         logits_sr=V, values=vals.data_ptr(), out=out.data_ptr(), out_sr=2 * k + 1)
+    stream = _lib.stream_of(dev)
+    t_kernel = EventTimer(torch).time(lambda: lib.rp_ply_topk(ctypes.byref(a), stream), 50)
+    t0 = time.perf_counter()
+    for _ in range(plies):
+        pb.push_tokens(tokens)
+        pb.pull(vals, cont)
+    t_ours = (time.perf_counter() - t0) / plies
+    t0 = time.perf_counter()
+    for _ in range(plies):
+        pb.pull_legal(cont, legal)
+    t_legal = (time.perf_counter() - t0) / plies
+
+    # the reference's per-ply pattern (engine/mars_search.py:262-265, :442-446, :475)
+    def ref_fixed():
+        tok_t = torch.tensor(tokens, dtype=torch.long, device=dev)
+        return tok_t, vals.detach().cpu().tolist()
+
+    def ref_rows(n):
+        for i in range(n):
+            ln = cont[i].float().cpu().numpy()
+            top = np.argpartition(ln, -k)[-k:]
+            top = top[np.argsort(ln[top])[::-1]]
+
+    def ref_legal_rows(n):
+        for i in range(n):
+            idx = torch.from_numpy(legal[i]).to(dev)
+            cont[i][idx].float().cpu().numpy()
+
+    ref_fixed(), ref_rows(8), ref_legal_rows(8)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        ref_fixed()
+    t_fixed = (time.perf_counter() - t0) / 5
+    t0 = time.perf_counter()
+    ref_rows(sample)
+    t_rows = (time.perf_counter() - t0) / sample
+    t0 = time.perf_counter()
+    ref_legal_rows(sample)
+    t_lrows = (time.perf_counter() - t0) / sample
+    return dict(t_kernel=t_kernel, kernel_bytes=R * V * 4 + R * 4 + R * (2 * k + 1) * 4,
+                t_ours=t_ours, t_legal=t_legal, t_ref=t_fixed + R * t_rows,
+                t_ref_legal=R * t_lrows, sample=sample)
 
 
 # One Eval-Mamba layer: d_model 768 (d_inner 1536), d_state 32 + 8, mimo_p 4,
@@ -922,6 +1007,15 @@ def main():
               f"({mix['bwd_bytes'] / mix['t_bwd'] / 1e9:.0f} GB/s); fwd+bwd autograd "
               f"{mix['t_fused'] * 1e6:.1f} us fused vs {mix['t_torch'] * 1e6:.1f} us torch ops",
               file=sys.stderr, flush=True)
+    roll = None
+    if not args.no_rollout:
+        roll = bench_rollout(torch, args)
+        print(f"[bench] rollout ply boundary (R={ROLLOUT_SHAPE['R']}, V={ROLLOUT_SHAPE['V']}): "
+              f"pinned {roll['t_ours'] * 1e3:.3f} ms/ply (top-k kernel "
+              f"{roll['t_kernel'] * 1e6:.1f} us, {roll['kernel_bytes'] / roll['t_kernel'] / 1e9:.0f} "
+              f"GB/s) vs per-rollout reads {roll['t_ref'] * 1e3:.1f} ms/ply; legal-move logits "
+              f"{roll['t_legal'] * 1e3:.3f} vs {roll['t_ref_legal'] * 1e3:.1f} ms/ply",
+              file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
@@ -1042,6 +1136,23 @@ def main():
             "timing": "each launch after a 512 MB read that displaces the last-level cache",
             "warm_cache_avg_launch_s": {"fwd": mix["t_fwd_warm"], "bwd": mix["t_bwd_warm"]},
             "fwd_bwd_autograd_s": {"fused": mix["t_fused"], "torch_ops": mix["t_torch"]},
+        }
+    if roll is not None:
+        line["rollout_boundary"] = {
+            "workload": "one ply's host transfers for 4096 lockstep rollouts: token ids up, "
+                        "values and each rollout's top-8 continuation candidates (8192-token "
+                        "vocabulary) down; and the fastchess path's logits of 40 legal moves "
+                        "per rollout",
+            **ROLLOUT_SHAPE,
+            "pinned_boundary_s_per_ply": roll["t_ours"],
+            "reference_pattern_s_per_ply": roll["t_ref"],
+            "legal_logits_s_per_ply": {"pinned": roll["t_legal"], "reference_pattern": roll["t_ref_legal"]},
+            "reference_sample": f"{roll['sample']} rollouts' row reads timed and scaled to R",
+            "kernel": {"name": "ply_topk_kernel", "avg_launch_s": roll["t_kernel"],
+                       "alg_bytes_per_launch": roll["kernel_bytes"],
+                       "achieved_GBps": roll["kernel_bytes"] / roll["t_kernel"] / 1e9,
+                       "frac": roll["kernel_bytes"] / roll["t_kernel"] / 1e9 / HBM_PEAK_GBS},
+            "timing": "host wall clock per ply (perf_counter), the kernel by HIP events",
         }
     line["cpu_baseline"] = cpu
     print(json.dumps(line), flush=True)

@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 9
+#define RP_ABI_VERSION 10
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -299,6 +299,60 @@ int rp_rmsnorm_check(const rp_rmsnorm_args* a);
 /* The residual add and the next RMSNorm of Mamba.step's layer loop in one
  * pass; replaces x + out and RMSNorm's five elementwise and reduction ops. */
 int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream);
+
+/*
+ * Host boundary of one lockstep rollout ply.  The reference moves each
+ * rollout's continuation row (engine/mars_search.py:262, _select_move's
+ * cont_logits.float().cpu()), the logits of its legal moves (:475,
+ * _select_fc_move) and the ply's values (:446, :556, vals.cpu().tolist())
+ * to the host one rollout at a time; these reduce and pack them on the
+ * device, so that one device-to-host copy per ply carries the ply.
+ *
+ * rp_ply_topk: per rollout r, the k largest logits of row r (IEEE total
+ * order, so a positive NaN ranks above +inf; equal logits by ascending token
+ * id) and the rollout's value, as row r of `out` in 32-bit words:
+ *     word 0          values[r] (fp32; 0 when values is NULL)
+ *     words 1 .. k    the logits, fp32, largest first (-inf past V)
+ *     words k+1 .. 2k their token ids, int32 (-1 past V)
+ * logits: (R, V) in dtype_logits with row stride logits_sr (elements);
+ * values: NULL or (R,) fp32; out: (R, out_sr) words, out_sr >= 2k + 1.
+ * 1 <= k <= 16.  This is _select_move's candidate list (np.argpartition over
+ * the row, then sorted by logit) for every rollout at once.
+ */
+typedef struct rp_ply_topk_args {
+  int64_t R, V;
+  int32_t k, dtype_logits;
+  const void* logits;  int64_t logits_sr;
+  const float* values;
+  void* out;           int64_t out_sr;
+} rp_ply_topk_args;
+
+/* Validate rp_ply_topk arguments on the host without launching anything. */
+int rp_ply_topk_check(const rp_ply_topk_args* a);
+
+/* Top-k continuation candidates and values of a ply, packed per rollout. */
+int rp_ply_topk(const rp_ply_topk_args* a, void* stream);
+
+/*
+ * rp_ply_gather: out[r, j] = logits[r, tokens[r, j]] as fp32 for j < M, and
+ * -inf for ids outside [0, V) (padding): _select_fc_move's gather of the
+ * legal moves' logits (engine/mars_search.py:475) for all rollouts at once.
+ * tokens: (R, M) int32 with row stride tokens_sr; out: (R, M) fp32 with row
+ * stride out_sr; logits as in rp_ply_topk.
+ */
+typedef struct rp_ply_gather_args {
+  int64_t R, V, M;
+  int32_t dtype_logits, reserved;
+  const void* logits;     int64_t logits_sr;
+  const int32_t* tokens;  int64_t tokens_sr;
+  float* out;             int64_t out_sr;
+} rp_ply_gather_args;
+
+/* Validate rp_ply_gather arguments on the host without launching anything. */
+int rp_ply_gather_check(const rp_ply_gather_args* a);
+
+/* The legal moves' logits of every rollout of a ply. */
+int rp_ply_gather(const rp_ply_gather_args* a, void* stream);
 
 /* ABI version this library was built with (RP_ABI_VERSION). */
 int rp_abi_version(void);

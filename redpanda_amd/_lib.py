@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -102,6 +102,21 @@ class RmsNormArgs(ctypes.Structure):
     ]
 
 
+class PlyTopkArgs(ctypes.Structure):
+    _fields_ = [
+        ("R", _i64), ("V", _i64), ("k", _i32), ("dtype_logits", _i32),
+        ("logits", _vp), ("logits_sr", _i64), ("values", _vp), ("out", _vp), ("out_sr", _i64),
+    ]
+
+
+class PlyGatherArgs(ctypes.Structure):
+    _fields_ = [
+        ("R", _i64), ("V", _i64), ("M", _i64), ("dtype_logits", _i32), ("reserved", _i32),
+        ("logits", _vp), ("logits_sr", _i64), ("tokens", _vp), ("tokens_sr", _i64),
+        ("out", _vp), ("out_sr", _i64),
+    ]
+
+
 # Every symbol include/redpanda_hip.h declares, with its ctypes signature.
 SIGNATURES = {
     "rp_abi_version": (ctypes.c_int, []),
@@ -119,6 +134,10 @@ SIGNATURES = {
     "rp_bcnorm_bwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), ctypes.POINTER(BcNormGrad), _vp]),
     "rp_rmsnorm_check": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs)]),
     "rp_rmsnorm_fwd": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs), _vp]),
+    "rp_ply_topk_check": (ctypes.c_int, [ctypes.POINTER(PlyTopkArgs)]),
+    "rp_ply_topk": (ctypes.c_int, [ctypes.POINTER(PlyTopkArgs), _vp]),
+    "rp_ply_gather_check": (ctypes.c_int, [ctypes.POINTER(PlyGatherArgs)]),
+    "rp_ply_gather": (ctypes.c_int, [ctypes.POINTER(PlyGatherArgs), _vp]),
     "rp_mixer_out_check": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs)]),
     "rp_mixer_out_work_bytes": (_i64, [ctypes.POINTER(MixerOutArgs)]),
     "rp_mixer_out_fwd": (ctypes.c_int, [ctypes.POINTER(MixerOutArgs), _vp]),

@@ -848,4 +848,87 @@ int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream) {
   return RP_OK;
 }
 
+int rp_ply_topk_check(const rp_ply_topk_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "ply topk args: NULL");
+  if (a->R < 0 || a->V < 1) return fail(RP_ERR_INVALID, "ply topk args: R < 0 or V < 1");
+  if (a->V > kI32Max / 2) return fail(RP_ERR_UNSUPPORTED, "ply topk args: V must fit in int32");
+  if (a->k < 1 || a->k > rp::kPlyMaxK)
+    return fail(RP_ERR_UNSUPPORTED, "ply topk args: k=%d outside [1, %d]", a->k, rp::kPlyMaxK);
+  if (a->dtype_logits != RP_F32 && a->dtype_logits != RP_BF16 && a->dtype_logits != RP_F16)
+    return fail(RP_ERR_INVALID, "ply topk args: unknown dtype code %d", a->dtype_logits);
+  if (a->out_sr < 2 * (int64_t)a->k + 1)
+    return fail(RP_ERR_INVALID, "ply topk args: out row stride below 2k + 1");
+  if (a->R == 0) return RP_OK;
+  if (!a->logits || !a->out) return fail(RP_ERR_INVALID, "ply topk args: NULL logits / out");
+  if (a->logits_sr < a->V) return fail(RP_ERR_INVALID, "ply topk args: logits row stride below V");
+  const int64_t es = elem_size(a->dtype_logits);
+  if (!aligned(a->logits, es) || !aligned(a->out, 4) || (a->values && !aligned(a->values, 4)))
+    return fail(RP_ERR_INVALID, "ply topk args: misaligned pointer");
+  const int64_t ob = ((a->R - 1) * a->out_sr + 2 * a->k + 1) * 4;
+  const int64_t lb = ((a->R - 1) * a->logits_sr + a->V) * es;
+  if (overlaps(a->out, ob, a->logits, lb) || (a->values && overlaps(a->out, ob, a->values, a->R * 4)))
+    return fail(RP_ERR_INVALID, "ply topk args: out overlaps an input");
+  return RP_OK;
+}
+
+int rp_ply_topk(const rp_ply_topk_args* a, void* stream) {
+  int st = rp_ply_topk_check(a);
+  if (st != RP_OK) return st;
+  rp::PlyTopkParams p{};
+  p.R = a->R;
+  p.V = (int)a->V;
+  p.k = a->k;
+  p.dt = a->dtype_logits;
+  p.logits = a->logits;
+  p.lsr = a->logits_sr;
+  p.values = a->values;
+  p.out = a->out;
+  p.osr = a->out_sr;
+  hipError_t e = rp::launch_ply_topk(p, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "ply topk launch");
+  return RP_OK;
+}
+
+int rp_ply_gather_check(const rp_ply_gather_args* a) {
+  if (a == nullptr) return fail(RP_ERR_INVALID, "ply gather args: NULL");
+  if (a->R < 0 || a->M < 0 || a->V < 1)
+    return fail(RP_ERR_INVALID, "ply gather args: R or M negative, or V < 1");
+  if (a->V > kI32Max) return fail(RP_ERR_UNSUPPORTED, "ply gather args: V must fit in int32");
+  if (a->dtype_logits != RP_F32 && a->dtype_logits != RP_BF16 && a->dtype_logits != RP_F16)
+    return fail(RP_ERR_INVALID, "ply gather args: unknown dtype code %d", a->dtype_logits);
+  if (a->reserved != 0) return fail(RP_ERR_INVALID, "ply gather args: reserved must be 0");
+  if (a->R * a->M == 0) return RP_OK;
+  if (!a->logits || !a->tokens || !a->out)
+    return fail(RP_ERR_INVALID, "ply gather args: NULL logits / tokens / out");
+  if (a->logits_sr < a->V || a->tokens_sr < a->M || a->out_sr < a->M)
+    return fail(RP_ERR_INVALID, "ply gather args: a row stride below its row length");
+  const int64_t es = elem_size(a->dtype_logits);
+  if (!aligned(a->logits, es) || !aligned(a->tokens, 4) || !aligned(a->out, 4))
+    return fail(RP_ERR_INVALID, "ply gather args: misaligned pointer");
+  const int64_t ob = ((a->R - 1) * a->out_sr + a->M) * 4;
+  if (overlaps(a->out, ob, a->logits, ((a->R - 1) * a->logits_sr + a->V) * es) ||
+      overlaps(a->out, ob, a->tokens, ((a->R - 1) * a->tokens_sr + a->M) * 4))
+    return fail(RP_ERR_INVALID, "ply gather args: out overlaps an input");
+  return RP_OK;
+}
+
+int rp_ply_gather(const rp_ply_gather_args* a, void* stream) {
+  int st = rp_ply_gather_check(a);
+  if (st != RP_OK) return st;
+  rp::PlyGatherParams p{};
+  p.R = a->R;
+  p.M = a->M;
+  p.V = (int)a->V;
+  p.dt = a->dtype_logits;
+  p.logits = a->logits;
+  p.lsr = a->logits_sr;
+  p.tokens = a->tokens;
+  p.tsr = a->tokens_sr;
+  p.out = a->out;
+  p.osr = a->out_sr;
+  hipError_t e = rp::launch_ply_gather(p, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "ply gather launch");
+  return RP_OK;
+}
+
 }  // extern "C"

@@ -1,0 +1,174 @@
+// Host boundary of one lockstep rollout ply, on the device side: what the
+// reference moves to the host row by row (engine/mars_search.py:262, the
+// continuation row of every rollout; :475, the logits of a rollout's legal
+// moves; :446 / :556, the rollout values) is reduced and packed here, so one
+// copy per ply carries it.
+//
+//   ply_topk:   per rollout row, the k largest logits with their token ids
+//               (descending; equal values by ascending id) and the value;
+//   ply_gather: per rollout, the logits of a padded list of token ids.
+//
+// ply_topk: one wave per row.  Lane l reads elements l, l + 64, ... (every
+// load coalesced) and keeps its own k largest as sorted 64-bit keys
+//     key = (order-preserving bits of the fp32 logit) << 32 | ~id,
+// so a larger key is a larger logit, or the smaller id of equal logits.  The
+// lanes' lists are then merged: k rounds of a wave max over the lanes' heads,
+// the winning lane shifting its list.  HBM-bound: V logits read once per row.
+
+#include <type_traits>
+
+#include "rp_device.h"
+#include "rp_launch.h"
+
+namespace rp {
+
+namespace {
+
+// fp32 bits -> uint32 whose unsigned order is the IEEE total order of the
+// floats (-NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN), and back.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return b ^ ((b & 0x80000000u) ? 0xffffffffu : 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __uint_as_float(k ^ ((k & 0x80000000u) ? 0x80000000u : 0xffffffffu));
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// A logit as fp32, the storage dtype fixed at compile time (a run-time
+// dtype branch per load would serialise the loads in flight).
+template <int DT>
+__device__ __forceinline__ float load_logit(const void* p, int64_t i) {
+  if constexpr (DT == RP_F32) {
+    return static_cast<const float*>(p)[i];
+  } else if constexpr (DT == RP_BF16) {
+    return __uint_as_float((uint32_t)static_cast<const uint16_t*>(p)[i] << 16);
+  } else {
+    return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  }
+}
+
+}  // namespace
+
+// KL: list length (k <= KL); each lane holds its KL largest keys, l[0] first.
+// Key 0 is below every element's key (an element's id part ~id is nonzero).
+constexpr int kPlyUnroll = 16;
+
+template <int KL, int DT>
+__global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + threadIdx.x / kWave;
+  if (row >= p.R) return;
+  uint64_t l[KL];
+#pragma unroll
+  for (int j = 0; j < KL; ++j) l[j] = 0;
+  const int64_t base = row * p.lsr;
+  // thr: the largest of the lanes' KL-th keys.  That lane holds KL keys at
+  // or above it, so no key at or below it is among the row's k <= KL
+  // largest; it only rises, and it lets most elements skip the insert.
+  uint64_t thr = 0;
+  // kPlyUnroll loads in flight per lane: a row is one wave's serial walk, so
+  // its memory latency is covered by loads in flight, not by other waves
+  for (int i0 = 0; i0 < p.V; i0 += kWave * kPlyUnroll) {
+    float v[kPlyUnroll];
+#pragma unroll
+    for (int u = 0; u < kPlyUnroll; ++u) {
+      const int i = i0 + u * kWave + lane;
+      v[u] = i < p.V ? load_logit<DT>(p.logits, base + i) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPlyUnroll; ++u) {
+      const int i = i0 + u * kWave + lane;
+      if (i >= p.V) break;
+      uint64_t x = ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i;
+      if (x > l[KL - 1] && x > thr) {
+        // sorted insert: the larger of (slot, carry) stays, the smaller moves on
+#pragma unroll
+        for (int j = 0; j < KL; ++j) {
+          const uint64_t hi = x > l[j] ? x : l[j];
+          x = x > l[j] ? l[j] : x;
+          l[j] = hi;
+        }
+      }
+    }
+    uint64_t w = l[KL - 1];
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+      const uint64_t o = shfl_xor_u64(w, s);
+      w = o > w ? o : w;
+    }
+    thr = w;
+  }
+  // merge: k rounds, each taking the largest head among the lanes
+  float myv = -__builtin_inff();
+  int myi = -1;
+  for (int m = 0; m < p.k; ++m) {
+    uint64_t w = l[0];
+#pragma unroll
+    for (int s = 1; s < kWave; s <<= 1) {
+      const uint64_t o = shfl_xor_u64(w, s);
+      w = o > w ? o : w;
+    }
+    if (lane == m && w != 0) {
+      myv = key_value((uint32_t)(w >> 32));
+      myi = (int)~(uint32_t)w;
+    }
+    if (w != 0 && l[0] == w) {
+#pragma unroll
+      for (int j = 0; j + 1 < KL; ++j) l[j] = l[j + 1];
+      l[KL - 1] = 0;
+    }
+  }
+  uint32_t* out = static_cast<uint32_t*>(p.out) + row * p.osr;
+  if (lane == 0) out[0] = p.values != nullptr ? __float_as_uint(p.values[row]) : 0u;
+  if (lane < p.k) {
+    out[1 + lane] = __float_as_uint(myv);
+    out[1 + p.k + lane] = (uint32_t)myi;
+  }
+}
+
+// out[r, j] = logits[r, tokens[r, j]] (fp32), -inf for ids outside [0, V).
+__global__ __launch_bounds__(kThreads) void ply_gather_kernel(PlyGatherParams p) {
+  const int64_t n = p.R * p.M;
+  for (int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * kThreads) {
+    const int64_t r = e / p.M, j = e % p.M;
+    const int32_t t = p.tokens[r * p.tsr + j];
+    p.out[r * p.osr + j] =
+        (t >= 0 && t < p.V) ? load_in(p.logits, r * p.lsr + t, p.dt) : -__builtin_inff();
+  }
+}
+
+hipError_t launch_ply_topk(const PlyTopkParams& p, hipStream_t st) {
+  if (p.R == 0) return hipSuccess;
+  const dim3 grid((unsigned)((p.R + kWaves - 1) / kWaves));
+  auto go = [&](auto dt_tag) {
+    constexpr int DT = decltype(dt_tag)::value;
+    if (p.k <= 8)
+      hipLaunchKernelGGL((ply_topk_kernel<8, DT>), grid, dim3(kThreads), 0, st, p);
+    else
+      hipLaunchKernelGGL((ply_topk_kernel<kPlyMaxK, DT>), grid, dim3(kThreads), 0, st, p);
+  };
+  if (p.dt == RP_F32)
+    go(std::integral_constant<int, RP_F32>{});
+  else if (p.dt == RP_BF16)
+    go(std::integral_constant<int, RP_BF16>{});
+  else
+    go(std::integral_constant<int, RP_F16>{});
+  return hipGetLastError();
+}
+
+hipError_t launch_ply_gather(const PlyGatherParams& p, hipStream_t st) {
+  const int64_t n = p.R * p.M;
+  if (n == 0) return hipSuccess;
+  const int64_t blocks = (n + kThreads - 1) / kThreads;
+  hipLaunchKernelGGL(ply_gather_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)),
+                     dim3(kThreads), 0, st, p);
+  return hipGetLastError();
+}
+
+}  // namespace rp

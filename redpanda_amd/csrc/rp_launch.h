@@ -213,6 +213,33 @@ hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc
 hipError_t launch_step(int S, int NPL, int gk, bool tile, const StepParams& p, hipStream_t st);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 
+// Rollout-ply boundary (ply.hip).
+constexpr int kPlyMaxK = 16;
+
+struct PlyTopkParams {
+  int64_t R;
+  int V, k, dt;
+  const void* logits;
+  int64_t lsr;           // logits row stride (elements)
+  const float* values;   // (R,) or null
+  void* out;             // (R, osr) 32-bit words: value, k logits, k ids
+  int64_t osr;
+};
+
+struct PlyGatherParams {
+  int64_t R, M;
+  int V, dt;
+  const void* logits;
+  int64_t lsr;
+  const int32_t* tokens;  // (R, M), row stride tsr
+  int64_t tsr;
+  float* out;             // (R, M), row stride osr
+  int64_t osr;
+};
+
+hipError_t launch_ply_topk(const PlyTopkParams& p, hipStream_t st);
+hipError_t launch_ply_gather(const PlyGatherParams& p, hipStream_t st);
+
 }  // namespace rp
 
 // Compiled (S, NPL) shapes: S lanes per channel, NPL states per lane.

@@ -213,7 +213,9 @@ def _header_struct_fields(name):
                                           ("rp_mixer_out_grad", "MixerOutGrad"),
                                           ("rp_bcnorm_args", "BcNormArgs"),
                                           ("rp_bcnorm_grad", "BcNormGrad"),
-                                          ("rp_rmsnorm_args", "RmsNormArgs")])
+                                          ("rp_rmsnorm_args", "RmsNormArgs"),
+                                          ("rp_ply_topk_args", "PlyTopkArgs"),
+                                          ("rp_ply_gather_args", "PlyGatherArgs")])
 def test_ctypes_structs_mirror_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
     assert py == _header_struct_fields(cname)
@@ -357,3 +359,36 @@ def test_rmsnorm_check(lib):
     assert chk(**{**add, "dtype_add": 4}) < 0
     assert chk(**{**add, "x_out": 0x400000}) < 0
     assert chk(rows=0, x=None, w=None, out=None) == 0
+
+
+def test_ply_topk_check(lib):
+    def chk(**kw):
+        a = _lib.PlyTopkArgs(R=4096, V=8192, k=8, dtype_logits=_lib.RP_F32, logits=0x1000000,
+                             logits_sr=8192, values=0x100, out=0x10000000, out_sr=17)
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return lib.rp_ply_topk_check(ctypes.byref(a))
+    assert chk() == 0
+    assert chk(k=0) < 0 and chk(k=17) < 0 and chk(k=16, out_sr=33) == 0
+    assert chk(out_sr=16) < 0
+    assert chk(V=0) < 0 and chk(logits_sr=8191) < 0
+    assert chk(dtype_logits=5) < 0
+    assert chk(dtype_logits=_lib.RP_BF16, logits=0x1000001) < 0
+    assert chk(out=0x1000000 + 64) < 0 and "overlaps" in lib.rp_last_error().decode()
+    assert chk(R=0, logits=None, out=None) == 0
+
+
+def test_ply_gather_check(lib):
+    def chk(**kw):
+        a = _lib.PlyGatherArgs(R=64, V=8192, M=40, dtype_logits=_lib.RP_BF16, logits=0x1000000,
+                               logits_sr=8192, tokens=0x100000, tokens_sr=40, out=0x200000,
+                               out_sr=40)
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return lib.rp_ply_gather_check(ctypes.byref(a))
+    assert chk() == 0
+    assert chk(reserved=1) < 0
+    assert chk(tokens_sr=39) < 0 and chk(out_sr=39) < 0
+    assert chk(tokens=0x100002) < 0
+    assert chk(out=0x100000) < 0
+    assert chk(M=0, tokens=None, out=None) == 0

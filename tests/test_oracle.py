@@ -319,3 +319,58 @@ def test_planted_error_is_caught():
     wrong = beta.sum(1)                              # forgot the 1/2 on the last token
     _, hL, _ = scan_ref.scan_sequential(dt, u, Bc, Cc, None, None, Tk)
     assert not torch.allclose(hL, wrong, rtol=1e-6)
+
+
+# ─── rollout ply host reads (oracle/rollout_ref.py) ─────────────────────────
+
+def test_rollout_candidates_match_reference_expression():
+    """On tie-free rows the oracle's candidate list is exactly the reference's
+    argpartition / argsort expression (engine/mars_search.py:262-265)."""
+    import numpy as np
+    from oracle import rollout_ref
+    rng = np.random.default_rng(0)
+    for V, k in [(8192, 8), (100, 8), (7, 8), (1, 1), (64, 16), (3000, 5)]:
+        row = rng.standard_normal(V).astype(np.float32)
+        ids, lns = rollout_ref.candidates(row, k)
+        assert np.array_equal(ids, rollout_ref.candidates_reference_expr(row, k))
+        assert np.array_equal(lns, row[ids])
+
+
+def test_rollout_candidates_brute_force_and_ties():
+    """Brute force on tiny rows: the list is the k largest, descending, equal
+    logits by ascending id; nothing outside beats anything inside.  A planted
+    wrong order (ascending) fails the same check."""
+    import itertools
+    import numpy as np
+    from oracle import rollout_ref
+    rng = np.random.default_rng(1)
+    for _ in range(200):
+        V = int(rng.integers(1, 9))
+        k = int(rng.integers(1, 6))
+        row = rng.integers(-2, 3, V).astype(np.float32)  # many ties
+        ids, lns = rollout_ref.candidates(row, k)
+        pairs = sorted(((-float(row[i]), i) for i in range(V)))[:min(k, V)]
+        assert [p[1] for p in pairs] == list(ids)
+        rest = set(range(V)) - set(ids.tolist())
+        assert all(row[j] <= lns.min() for j in rest)
+        # a planted mistake (the k smallest, ascending) fails the same check
+        wrong = sorted(((float(row[i]), i) for i in range(V)))[:min(k, V)]
+        if len(set(row.tolist())) > 1:
+            assert [p[1] for p in wrong] != list(ids)
+
+
+def test_rollout_gather_and_select_walk():
+    import numpy as np
+    from oracle import rollout_ref
+    row = np.arange(10, dtype=np.float32) * 0.5
+    assert np.array_equal(rollout_ref.gather_legal(row, [3, -1, 9, 10]),
+                          np.array([1.5, -np.inf, 4.5, -np.inf], dtype=np.float32))
+    # greedy: the first legal candidate, largest logit first
+    assert rollout_ref.select_move(row, 4, lambda t: t % 2 == 0, 0.0, None) == 8
+    assert rollout_ref.select_move(row, 4, lambda t: False, 0.0, None) is None
+    # the draw: a softmax over the legal candidates, one rng.choice call
+    a = rollout_ref.select_move(row, 4, lambda t: t != 9, 0.6, np.random.default_rng(5))
+    lg = np.array([4.0, 3.5, 3.0]) / 0.6
+    lg -= lg.max()
+    pr = np.exp(lg) / np.exp(lg).sum()
+    assert a == [8, 7, 6][int(np.random.default_rng(5).choice(3, p=pr))]
