@@ -11,9 +11,12 @@
 // ply_topk: one wave per row.  Lane l reads elements l, l + 64, ... (every
 // load coalesced) and keeps its own k largest as sorted 64-bit keys
 //     key = (order-preserving bits of the fp32 logit) << 32 | ~id,
-// so a larger key is a larger logit, or the smaller id of equal logits.  The
-// lanes' lists are then merged: k rounds of a wave max over the lanes' heads,
-// the winning lane shifting its list.  HBM-bound: V logits read once per row.
+// so a larger key is a larger logit, or the smaller id of equal logits.  A
+// wave-wide lower bound on the row's k-th key (from a sort of the lane
+// maxima across the wave) lets most elements skip the insert after one
+// float compare.  The lanes' lists are then merged: k rounds of a wave max
+// over the lanes' heads, the winning lane shifting its list.  V logits are
+// read once per row.
 
 #include <type_traits>
 
@@ -67,23 +70,27 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
 #pragma unroll
   for (int j = 0; j < KL; ++j) l[j] = 0;
   const int64_t base = row * p.lsr;
-  // thr: the largest of the lanes' KL-th keys.  That lane holds KL keys at
-  // or above it, so no key at or below it is among the row's k <= KL
-  // largest; it only rises, and it lets most elements skip the insert.
+  // thr: the KL-th largest of the lanes' largest keys.  KL distinct
+  // elements (those lane maxima) are at or above it, so no key below it is
+  // among the row's k <= KL largest.  thr_f, its logit, filters elements
+  // with one float compare: one below it can be skipped (a NaN or a logit
+  // equal to it takes the exact 64-bit test).
   uint64_t thr = 0;
-  // kPlyUnroll loads in flight per lane: a row is one wave's serial walk, so
-  // its memory latency is covered by loads in flight, not by other waves
-  for (int i0 = 0; i0 < p.V; i0 += kWave * kPlyUnroll) {
-    float v[kPlyUnroll];
+  float thr_f = -__builtin_inff();
+  auto load_block = [&](int i0, float (&v)[kPlyUnroll]) {
 #pragma unroll
     for (int u = 0; u < kPlyUnroll; ++u) {
       const int i = i0 + u * kWave + lane;
       v[u] = i < p.V ? load_logit<DT>(p.logits, base + i) : 0.f;
     }
+  };
+  int nb = 0;  // blocks taken
+  auto take_block = [&](int i0, const float (&v)[kPlyUnroll]) {
 #pragma unroll
     for (int u = 0; u < kPlyUnroll; ++u) {
       const int i = i0 + u * kWave + lane;
       if (i >= p.V) break;
+      if (v[u] < thr_f) continue;
       uint64_t x = ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i;
       if (x > l[KL - 1] && x > thr) {
         // sorted insert: the larger of (slot, carry) stays, the smaller moves on
@@ -95,13 +102,40 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
         }
       }
     }
-    uint64_t w = l[KL - 1];
+    // the bound is refreshed after blocks 1, 2, 4, 8, ...: it tightens
+    // fastest early, and each refresh is a 21-stage exchange across the wave
+    const bool refresh = (nb & (nb + 1)) == 0;
+    ++nb;
+    if (!refresh) return;
+    // bitonic sort of the lane maxima across the wave (ascending by lane),
+    // then the KL-th largest is lane 64 - KL's
+    uint64_t w = l[0];
 #pragma unroll
-    for (int s = 1; s < kWave; s <<= 1) {
-      const uint64_t o = shfl_xor_u64(w, s);
-      w = o > w ? o : w;
+    for (int kk = 2; kk <= kWave; kk <<= 1) {
+#pragma unroll
+      for (int j = kk >> 1; j > 0; j >>= 1) {
+        const uint64_t o = shfl_xor_u64(w, j);
+        const bool keep_min = ((lane & j) == 0) == ((lane & kk) == 0);
+        w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
+      }
     }
-    thr = w;
+    const uint32_t tlo = __shfl((uint32_t)w, kWave - KL);
+    const uint32_t thi = __shfl((uint32_t)(w >> 32), kWave - KL);
+    thr = ((uint64_t)thi << 32) | tlo;
+    if (thr != 0) thr_f = key_value(thi);
+  };
+  // A row is one wave's serial walk, so its memory latency is covered by
+  // loads in flight: kPlyUnroll per lane, and the next block's loads issued
+  // before the current block is taken (two register buffers, alternating).
+  constexpr int kBlock = kWave * kPlyUnroll;
+  float va[kPlyUnroll], vb[kPlyUnroll];
+  load_block(0, va);
+  for (int i0 = 0; i0 < p.V; i0 += 2 * kBlock) {
+    if (i0 + kBlock < p.V) load_block(i0 + kBlock, vb);
+    take_block(i0, va);
+    if (i0 + kBlock >= p.V) break;
+    if (i0 + 2 * kBlock < p.V) load_block(i0 + 2 * kBlock, va);
+    take_block(i0 + kBlock, vb);
   }
   // merge: k rounds, each taking the largest head among the lanes
   float myv = -__builtin_inff();
