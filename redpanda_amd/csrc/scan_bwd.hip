@@ -56,6 +56,15 @@ constexpr int kParChunks = 16;
 template <int S, int NPL, class GK>
 __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
   using Sh = Shape<S, NPL>;
+  // ALT: the entry state is prefetched into two buffers that alternate with
+  // the LDS slot (the chunk in slot SL enters from buffer SL and loads the
+  // next chunk's entry into the other), and a chunk takes its entry before
+  // it issues its own loads.  Loads complete in issue order, so a wait for a
+  // single prefetch buffer, copied after the chunk's loads were issued, had
+  // to wait for those loads too.  The second buffer costs registers: only
+  // instantiations with room take it (without spills).
+  constexpr bool ALT = NPL <= 3 || (NPL == 4 && S >= 8) ||
+                       (NPL == 5 && S == 8 && GK::kRJ == NPL - 1 && GK::kTJ == NPL - 1);
   constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, K = kCkptK;
   constexpr int KR = NP <= 40 ? K : K / 2;  // steps per channel-sum fold
   constexpr int NFOLD = K / KR;             // folds per chunk
@@ -247,9 +256,13 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
         cpt[j] = 0.f;
       }
       // the entry state of the next chunk to process, loaded one chunk ahead
-      float hnx[NPL];
+      // (with ALT, into the buffer of that chunk's LDS slot)
+      float hE[ALT ? 2 : 1][NPL];
       if (nct > 0) {
-        load_entry_h(nct - 1, b, dir, hnx);
+        if (ALT && (nct - 1) % 2 == 1)
+          load_entry_h(nct - 1, b, dir, hE[ALT ? 1 : 0]);
+        else
+          load_entry_h(nct - 1, b, dir, hE[0]);
         // stage the sweep's first chunk (the slots are free: the previous
         // sweep ended with a barrier)
         stage_load(b, dir, nct - 1);
@@ -263,46 +276,60 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       for (int ch = nct - 1; ch >= 0; --ch) {
         const int i0 = ch * K;
         const int kcnt = min(K, L - i0);
-        // loads a chunk ahead: the inputs of chunk ch-1, and the partials the
-        // reverse direction adds to (dB / dC and d_delta / d_u)
-        if (ch >= 1) stage_load(b, dir, ch - 1);
         float prev[NFOLD][FPT], pdd[DPT][2];
-#pragma unroll
-        for (int f = 0; f < NFOLD; ++f) {
-#pragma unroll
-          for (int k = 0; k < FPT; ++k) {
-            prev[f][k] = 0.f;
-            if (dir == 1) {
-              const float* src = fold_dst(tid + k * kThreads, b, dir, i0, f * KR, kcnt);
-              if (src != nullptr) prev[f][k] = *src;
-            }
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < DPT; ++k) {
-          pdd[k][0] = 0.f;
-          pdd[k][1] = 0.f;
-          if (dir == 1) {
-            const int64_t idx = dd_index(tid + k * kThreads, b, dir, i0, kcnt);
-            if (idx >= 0) {
-              pdd[k][0] = io.d_delta[idx];
-              pdd[k][1] = io.d_u[idx];
-            }
-          }
-        }
-        // state entering the chunk: h as prefetched, hb from the step before
-        // (row 0 of the slot; zero before the first step) or, for chunk 0 of
-        // a causal scan from a given state, from beta0
         float hc[NPL], hbp[NPL];
+        // loads a chunk ahead: the inputs of chunk ch-1, the partials the
+        // reverse direction adds to (dB / dC and d_delta / d_u), and the
+        // state entering chunk ch-1 (into `next`)
+        auto issue_loads = [&](float (&next)[NPL]) {
+          if (ch >= 1) stage_load(b, dir, ch - 1);
 #pragma unroll
-        for (int j = 0; j < NPL; ++j) hc[j] = hnx[j];
-        if (ch > 0) load_entry_h(ch - 1, b, dir, hnx);
+          for (int f = 0; f < NFOLD; ++f) {
+#pragma unroll
+            for (int k = 0; k < FPT; ++k) {
+              prev[f][k] = 0.f;
+              if (dir == 1) {
+                const float* src = fold_dst(tid + k * kThreads, b, dir, i0, f * KR, kcnt);
+                if (src != nullptr) prev[f][k] = *src;
+              }
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < DPT; ++k) {
+            pdd[k][0] = 0.f;
+            pdd[k][1] = 0.f;
+            if (dir == 1) {
+              const int64_t idx = dd_index(tid + k * kThreads, b, dir, i0, kcnt);
+              if (idx >= 0) {
+                pdd[k][0] = io.d_delta[idx];
+                pdd[k][1] = io.d_u[idx];
+              }
+            }
+          }
+          if (ch > 0) load_entry_h(ch - 1, b, dir, next);
+        };
+        if constexpr (!ALT) {
+          // the entry state is copied out of the one prefetch buffer, which
+          // then receives the next chunk's
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) hc[j] = hE[0][j];
+          issue_loads(hE[0]);
+        }
         // The chunk body, instantiated for FULL (all K steps present, the
         // common case; straight-line code) or a guarded tail for a last chunk
         // shorter than K, and for the LDS slot SL that holds the chunk.
         auto chunk_body = [&](auto full_tag, auto slot_tag) {
           constexpr bool FULL = decltype(full_tag)::value;
           constexpr int SL = decltype(slot_tag)::value;
+          if constexpr (ALT) {
+            // the entry state, taken before this chunk issues its loads
+#pragma unroll
+            for (int j = 0; j < NPL; ++j) hc[j] = hE[SL][j];
+            issue_loads(hE[1 - SL]);
+          }
+          // hb entering the chunk: from the step before (row 0 of the slot;
+          // zero before the first step) or, for chunk 0 of a causal scan from
+          // a given state, from beta0
           if (ch == 0) {
 #pragma unroll
             for (int j = 0; j < NPL; ++j) {
