@@ -816,6 +816,18 @@ def profile_pass(torch):
         _lib.check(lib.rp_bcnorm_bwd(ctypes.byref(ba), ctypes.byref(bgr), stream), lib)
     torch.cuda.synchronize()
     del xd, bo, bg_t
+    # the rollout ply's top-k at the rollout shape, three dispatches
+    sh = ROLLOUT_SHAPE
+    logits = torch.randn(sh["R"], sh["V"], device=dev)
+    vals = torch.randn(sh["R"], device=dev)
+    pk = torch.empty(sh["R"], 2 * sh["k"] + 1, device=dev)
+    pa = _lib.PlyTopkArgs(R=sh["R"], V=sh["V"], k=sh["k"], dtype_logits=_lib.RP_F32,
+                          logits=logits.data_ptr(), logits_sr=sh["V"], values=vals.data_ptr(),
+                          out=pk.data_ptr(), out_sr=2 * sh["k"] + 1)
+    for _ in range(3):
+        _lib.check(lib.rp_ply_topk(ctypes.byref(pa), stream), lib)
+    torch.cuda.synchronize()
+    del logits, vals, pk
     print(f"[bench] profile pass done: scan fwd/bwd x3, step x{step_layers}, "
           f"calibration neg {src.numel() * 4} bytes each way", file=sys.stderr, flush=True)
 
