@@ -106,10 +106,10 @@ __device__ __forceinline__ float ffma(float a, float b, float c) { return __buil
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // The gate tables copied into LDS once per workgroup (read after the
-// workgroup's next barrier): the cos records (forward and step) or the
-// (cos, sin) pairs (backward) of the kTab table angles 2 pi k / kTab.
-__device__ __forceinline__ void fill_cos_records(float4* ctab, int tid) {
-  for (int k = tid; k < kTab; k += kThreads) ctab[k] = kCosRec[k];
+// workgroup's next barrier): the (cos, -sin a) pairs (forward and step) or
+// the (cos, sin) pairs (backward) of the kTab table angles 2 pi k / kTab.
+__device__ __forceinline__ void fill_cos_lin(float2* ctab, int tid) {
+  for (int k = tid; k < kTab; k += kThreads) ctab[k] = kCosLin[k];
 }
 __device__ __forceinline__ void fill_sincos_pairs(float2* cstab, int tid) {
   for (int k = tid; k < kTab; k += kThreads) cstab[k] = kSinCos[k];
@@ -193,8 +193,9 @@ __device__ __forceinline__ int angle_split(float dt, float wh, float& r) {
 // Two flavours of the same expansion, in two phases each so that a caller
 // can start the exponentials and table reads of several states before
 // finishing any of them (issue, then finish):
-//   * the forward and the step: cos from the index's cos record (one 16-byte
-//     table read, three FMAs);
+//   * the forward and the step: cos as the cubic in r from the index's
+//     (c, -s a) (one 8-byte table read; the two higher coefficients one
+//     multiply each, then three FMAs);
 //   * the backward: cos and also es = 2^(dt pah) sin(a dt wh) from the
 //     index's (cos, sin) pair (one 8-byte read; the two expansions share r^2,
 //     cos - 1 and sin of the remainder).  Its gate is the forward's to
@@ -202,7 +203,7 @@ __device__ __forceinline__ int angle_split(float dt, float wh, float& r) {
 struct GatePart {
   float e;    // 2^(dt pah)
   float r;    // angle remainder, |r| <= 1/2 (table steps)
-  float4 cr;  // cos record of the table angle
+  float2 cr;  // (c, -s a) of the table angle
 };
 
 struct GatePartCS {
@@ -212,12 +213,12 @@ struct GatePartCS {
 };
 
 __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh, bool imag,
-                                                   const float4* ctab) {
+                                                   const float2* ctab) {
   GatePart g;
   g.e = exp2_hw(fmul(dt, pah));
   if (!imag) {
     g.r = 0.f;
-    g.cr = make_float4(1.f, 0.f, 0.f, 0.f);
+    g.cr = make_float2(1.f, 0.f);
     return g;
   }
   g.cr = ctab[angle_split(dt, wh, g.r)];
@@ -227,7 +228,10 @@ __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh
 __device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag) {
   if (!imag) return g.e;
   const float r = g.r;
-  return fmul(g.e, ffma(r, ffma(r, ffma(r, g.cr.w, g.cr.z), g.cr.y), g.cr.x));
+  // cos(a (k + r)) = c + r (-s a + r (c kC2 + r (-s a) kA3)), kA3 = -a^2/6
+  constexpr float kA3 = -1.0039880779102944e-4f;
+  const float p3 = fmul(g.cr.y, kA3), p2 = fmul(g.cr.x, kC2);
+  return fmul(g.e, ffma(r, ffma(r, ffma(r, p3, p2), g.cr.y), g.cr.x));
 }
 
 __device__ __forceinline__ GatePartCS rot_gate_issue_cs(float dt, float pah, float wh, bool imag,
@@ -285,7 +289,7 @@ __device__ __forceinline__ bool imag_of(bool has_imag) {
 // carry 0 and B = C = 0).
 template <int S, class GK>
 __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pah,
-                                         float wh, const float4* ctab) {
+                                         float wh, const float2* ctab) {
   if (j >= GK::kTJ) return pah;
   const bool imag = imag_of<GK>(has_imag);
   if (j < GK::kRJ) return rot_gate_finish(rot_gate_issue(dt, pah, wh, imag, ctab), imag);
@@ -345,7 +349,7 @@ __device__ __forceinline__ void load_gate_regs(GateRegs<NPL>& gp, const float* A
 // previous step's hb.  Shared verbatim by the scan and step kernels.
 template <int S, int NPL, class GK>
 __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
-                                            const GateRegs<NPL>& gp, const float4* ctab, float dt,
+                                            const GateRegs<NPL>& gp, const float2* ctab, float dt,
                                             float hdu, const float* __restrict__ Bs,
                                             const float* __restrict__ Cs, int s, int NR,
                                             bool has_imag) {
@@ -370,7 +374,7 @@ __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
 template <int S, int NPL, class GK>
 __device__ __forceinline__ float fwd_update_carried(float (&sm)[NPL], float (&hn)[NPL],
                                                     float (&hbn)[NPL], const GateRegs<NPL>& gp,
-                                                    const float4* ctab, float dt, float hdu,
+                                                    const float2* ctab, float dt, float hdu,
                                                     const float* __restrict__ Bs,
                                                     const float* __restrict__ Cs, int s, int NR,
                                                     bool has_imag) {

@@ -19,10 +19,9 @@
 // registers (keeping s_{t-1}, the gate and e*sin, so the adjoint evaluates
 // no transcendental), then runs the adjoint over them.  The recompute
 // evaluates the forward's gate expansion from (cos, sin) table pairs, which
-// also gives the sine (an 8-byte table read, where the forward's 16-byte cos
-// record would double the LDS traffic of a kernel that already shares the
-// LDS with its reductions); each gate matches the forward's to within an ulp
-// and every chunk restarts from the forward's checkpoint.
+// also give the sine (one 8-byte table read; the forward's (cos, -sin a)
+// pairs would need a second read for it); each gate matches the forward's to
+// within an ulp and every chunk restarts from the forward's checkpoint.
 //
 // Streaming: the per-step inputs (dt, (dt*u)/2, u, dy per channel; B, C per
 // state) of a chunk and of the step before it sit in one of two LDS slots.

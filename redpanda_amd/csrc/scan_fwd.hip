@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
   __shared__ float sY[TB][CB];     // the block's y, written out channel-contiguous
-  __shared__ float4 sCos[kTab];      // cos records of the gate table
+  __shared__ float2 sCos[kTab];      // (cos, -sin a) pairs of the gate table
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
 
   GateRegs<NPL> gp;  // loads issued first, so the table copy overlaps them
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
-  fill_cos_records(sCos, tid);  // first read after the staging barrier below
+  fill_cos_lin(sCos, tid);  // first read after the staging barrier below
 
   const int nblk = (L + TB - 1) / TB;
   for (int dir = 0; dir < p.ndir; ++dir) {
