@@ -145,13 +145,20 @@ class PlyBoundary:
         if R != self.R or M > self.max_legal:
             raise ValueError(f"PlyBoundary.pull_legal: tokens {tokens.shape}, expected ({self.R}, "
                              f"<= {self.max_legal})")
-        self._leg_h.numpy()[:, :M] = tokens
-        self._leg_d[:, :M].copy_(self._leg_h[:, :M], non_blocking=True)
-        ply_gather(cont, self._leg_d[:, :M], out=self._lout_d[:, :M])
-        self._lout_h[:, :M].copy_(self._lout_d[:, :M], non_blocking=True)
+        # (R, M) views of the flat buffers, contiguous, so each copy is one
+        # contiguous transfer
+        n = R * M
+        leg_h = self._leg_h.view(-1)[:n].view(R, M)
+        leg_d = self._leg_d.view(-1)[:n].view(R, M)
+        lout_d = self._lout_d.view(-1)[:n].view(R, M)
+        lout_h = self._lout_h.view(-1)[:n].view(R, M)
+        leg_h.numpy()[:] = tokens
+        leg_d.copy_(leg_h, non_blocking=True)
+        ply_gather(cont, leg_d, out=lout_d)
+        lout_h.copy_(lout_d, non_blocking=True)
         self._event.record()
         self._event.synchronize()
-        return self._lout_h.numpy()[:, :M]
+        return lout_h.numpy()
 
 
 def select_policy_move(top_ids, top_logits, is_legal, rollout_temp, rng=np.random):
