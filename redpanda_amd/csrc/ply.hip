@@ -70,9 +70,9 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
 #pragma unroll
   for (int j = 0; j < KL; ++j) l[j] = 0;
   const int64_t base = row * p.lsr;
-  // thr: the KL-th largest of the lanes' largest keys.  KL distinct
-  // elements (those lane maxima) are at or above it, so no key below it is
-  // among the row's k <= KL largest.  thr_f, its logit, filters elements
+  // thr: the KL-th largest logit among the lanes' largest keys.  KL
+  // distinct elements (those lane maxima) have that logit or a larger one,
+  // so no element with a smaller logit is among the row's k <= KL largest.  thr_f, its logit, filters elements
   // with one float compare: one below it can be skipped (a NaN or a logit
   // equal to it takes the exact 64-bit test).
   uint64_t thr = 0;
@@ -107,22 +107,23 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
     const bool refresh = (nb & (nb + 1)) == 0;
     ++nb;
     if (!refresh) return;
-    // bitonic sort of the lane maxima across the wave (ascending by lane),
-    // then the KL-th largest is lane 64 - KL's
-    uint64_t w = l[0];
+    // bitonic sort of the lane maxima's logit keys (the upper halves; ids do
+    // not matter for a bound) across the wave, ascending by lane; the KL-th
+    // largest is lane 64 - KL's.  thr keeps every element with that logit
+    // or a larger one (its id half is zero, below any element's)
+    uint32_t w = (uint32_t)(l[0] >> 32);
 #pragma unroll
     for (int kk = 2; kk <= kWave; kk <<= 1) {
 #pragma unroll
       for (int j = kk >> 1; j > 0; j >>= 1) {
-        const uint64_t o = shfl_xor_u64(w, j);
+        const uint32_t o = __shfl_xor(w, j);
         const bool keep_min = ((lane & j) == 0) == ((lane & kk) == 0);
-        w = keep_min ? (o < w ? o : w) : (o > w ? o : w);
+        w = keep_min ? min(o, w) : max(o, w);
       }
     }
-    const uint32_t tlo = __shfl((uint32_t)w, kWave - KL);
-    const uint32_t thi = __shfl((uint32_t)(w >> 32), kWave - KL);
-    thr = ((uint64_t)thi << 32) | tlo;
-    if (thr != 0) thr_f = key_value(thi);
+    const uint32_t thi = __shfl(w, kWave - KL);
+    thr = (uint64_t)thi << 32;
+    if (thi != 0) thr_f = key_value(thi);
   };
   // A row is one wave's serial walk, so its memory latency is covered by
   // loads in flight: kPlyUnroll per lane, and the next block's loads issued
