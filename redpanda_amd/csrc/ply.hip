@@ -11,10 +11,10 @@
 // ply_topk: one wave per row.  Lane l reads elements l, l + 64, ... (every
 // load coalesced) and keeps its own k largest as sorted 64-bit keys
 //     key = (order-preserving bits of the fp32 logit) << 32 | ~id,
-// so a larger key is a larger logit, or the smaller id of equal logits.  A
-// wave-wide lower bound on the row's k-th key (from a sort of the lane
-// maxima across the wave) lets most elements skip the insert after one
-// float compare.  The lanes' lists are then merged: k rounds of a wave max
+// so a larger key is a larger logit, or the smaller id of equal logits.  The
+// first block fills the lists with a sorting network; after it, a wave-wide
+// lower bound on the row's k-th logit (from a sort of the lane maxima across
+// the wave) lets most elements skip the insert after one float compare.  The lanes' lists are then merged: k rounds of a wave max
 // over the lanes' heads, the winning lane shifting its list.  V logits are
 // read once per row.
 
@@ -86,19 +86,51 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
   };
   int nb = 0;  // blocks taken
   auto take_block = [&](int i0, const float (&v)[kPlyUnroll]) {
+    if (nb == 0) {
+      // the first block fills the (empty) lists: its keys sorted, largest
+      // first, by a bitonic network in registers (elements past V: key 0)
+      static_assert(KL <= kPlyUnroll, "the first block fills the list");
+      uint64_t x[kPlyUnroll];
 #pragma unroll
-    for (int u = 0; u < kPlyUnroll; ++u) {
-      const int i = i0 + u * kWave + lane;
-      if (i >= p.V) break;
-      if (v[u] < thr_f) continue;
-      uint64_t x = ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i;
-      if (x > l[KL - 1] && x > thr) {
-        // sorted insert: the larger of (slot, carry) stays, the smaller moves on
+      for (int u = 0; u < kPlyUnroll; ++u) {
+        const int i = i0 + u * kWave + lane;
+        x[u] = i < p.V ? ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i : 0;
+      }
 #pragma unroll
-        for (int j = 0; j < KL; ++j) {
-          const uint64_t hi = x > l[j] ? x : l[j];
-          x = x > l[j] ? l[j] : x;
-          l[j] = hi;
+      for (int kk = 2; kk <= kPlyUnroll; kk <<= 1) {
+#pragma unroll
+        for (int j = kk >> 1; j > 0; j >>= 1) {
+#pragma unroll
+          for (int a = 0; a < kPlyUnroll; ++a) {
+            const int b = a ^ j;
+            if (b <= a) continue;
+            // descending runs where a & kk == 0, ascending elsewhere, so
+            // the last merge leaves the whole array descending
+            const bool desc = (a & kk) == 0;
+            const uint64_t lo = x[a] < x[b] ? x[a] : x[b];
+            const uint64_t hi = x[a] < x[b] ? x[b] : x[a];
+            x[a] = desc ? hi : lo;
+            x[b] = desc ? lo : hi;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < KL; ++j) l[j] = x[j];
+    } else {
+#pragma unroll
+      for (int u = 0; u < kPlyUnroll; ++u) {
+        const int i = i0 + u * kWave + lane;
+        if (i >= p.V) break;
+        if (v[u] < thr_f) continue;
+        uint64_t x = ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i;
+        if (x > l[KL - 1] && x > thr) {
+          // sorted insert: the larger of (slot, carry) stays, the smaller moves on
+#pragma unroll
+          for (int j = 0; j < KL; ++j) {
+            const uint64_t hi = x > l[j] ? x : l[j];
+            x = x > l[j] ? l[j] : x;
+            l[j] = hi;
+          }
         }
       }
     }
