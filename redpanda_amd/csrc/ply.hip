@@ -77,7 +77,13 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
   // equal to it takes the exact 64-bit test).
   uint64_t thr = 0;
   float thr_f = -__builtin_inff();
-  auto load_block = [&](int i0, float (&v)[kPlyUnroll]) {
+  // full blocks: unconditional loads at one address plus immediate offsets;
+  // the last, partial block: loads masked by the row length (0 beyond it)
+  auto load_full = [&](int i0, float (&v)[kPlyUnroll]) {
+#pragma unroll
+    for (int u = 0; u < kPlyUnroll; ++u) v[u] = load_logit<DT>(p.logits, base + i0 + lane + u * kWave);
+  };
+  auto load_part = [&](int i0, float (&v)[kPlyUnroll]) {
 #pragma unroll
     for (int u = 0; u < kPlyUnroll; ++u) {
       const int i = i0 + u * kWave + lane;
@@ -85,8 +91,14 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
     }
   };
   int nb = 0;  // blocks taken
-  auto take_block = [&](int i0, const float (&v)[kPlyUnroll]) {
-    if (nb == 0) {
+  auto take_block = [&](auto full, auto first, int i0, const float (&v)[kPlyUnroll]) {
+    constexpr bool kFull = decltype(full)::value;
+    // ~id of the block's slot u is idb - 64 u.  The empty asm makes idb
+    // opaque, so the compiler rebuilds each slot's id with one subtract
+    // instead of keeping 16 per-slot 64-bit constants live across the loop.
+    uint32_t idb = ~(uint32_t)(i0 + lane);
+    asm volatile("" : "+v"(idb));
+    if constexpr (decltype(first)::value) {
       // the first block fills the (empty) lists: its keys sorted, largest
       // first, by a bitonic network in registers (elements past V: key 0)
       static_assert(KL <= kPlyUnroll, "the first block fills the list");
@@ -94,7 +106,7 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
 #pragma unroll
       for (int u = 0; u < kPlyUnroll; ++u) {
         const int i = i0 + u * kWave + lane;
-        x[u] = i < p.V ? ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i : 0;
+        x[u] = (kFull || i < p.V) ? ((uint64_t)order_key(v[u]) << 32) | (idb - (uint32_t)(u * kWave)) : 0;
       }
 #pragma unroll
       for (int kk = 2; kk <= kPlyUnroll; kk <<= 1) {
@@ -120,9 +132,9 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
 #pragma unroll
       for (int u = 0; u < kPlyUnroll; ++u) {
         const int i = i0 + u * kWave + lane;
-        if (i >= p.V) break;
+        if (!kFull && i >= p.V) break;
         if (v[u] < thr_f) continue;
-        uint64_t x = ((uint64_t)order_key(v[u]) << 32) | (uint32_t)~(uint32_t)i;
+        uint64_t x = ((uint64_t)order_key(v[u]) << 32) | (idb - (uint32_t)(u * kWave));
         if (x > l[KL - 1] && x > thr) {
           // sorted insert: the larger of (slot, carry) stays, the smaller moves on
 #pragma unroll
@@ -160,15 +172,35 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
   // A row is one wave's serial walk, so its memory latency is covered by
   // loads in flight: kPlyUnroll per lane, and the next block's loads issued
   // before the current block is taken (two register buffers, alternating).
+  // The full blocks' loads carry no per-lane condition, so the loads of one
+  // block stay in flight while the other block is taken.
   constexpr int kBlock = kWave * kPlyUnroll;
+  const std::integral_constant<bool, true> full, first;
+  const std::integral_constant<bool, false> part, rest;
+  const int nfull = p.V / kBlock;
   float va[kPlyUnroll], vb[kPlyUnroll];
-  load_block(0, va);
-  for (int i0 = 0; i0 < p.V; i0 += 2 * kBlock) {
-    if (i0 + kBlock < p.V) load_block(i0 + kBlock, vb);
-    take_block(i0, va);
-    if (i0 + kBlock >= p.V) break;
-    if (i0 + 2 * kBlock < p.V) load_block(i0 + 2 * kBlock, va);
-    take_block(i0 + kBlock, vb);
+  int b = 0;
+  if (nfull > 0) {
+    // the first block, taken out of the loop (the sorting network is the
+    // largest code path; the loop holds only the filtered inserts)
+    load_full(0, va);
+    if (nfull > 1) load_full(kBlock, vb);
+    take_block(full, first, 0, va);
+    // block b is in vb on entry to each iteration
+    for (b = 1; b + 1 < nfull; b += 2) {
+      load_full((b + 1) * kBlock, va);
+      take_block(full, rest, b * kBlock, vb);
+      if (b + 2 < nfull) load_full((b + 2) * kBlock, vb);
+      take_block(full, rest, (b + 1) * kBlock, va);
+    }
+    if (b < nfull) take_block(full, rest, (b++) * kBlock, vb);
+  }
+  if (b * kBlock < p.V) {
+    load_part(b * kBlock, va);
+    if (b == 0)
+      take_block(part, first, 0, va);
+    else
+      take_block(part, rest, b * kBlock, va);
   }
   // merge: k rounds, each taking the largest head among the lanes
   float myv = -__builtin_inff();

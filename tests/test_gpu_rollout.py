@@ -44,8 +44,11 @@ def _check_topk(logits, k, values=None):
             assert h[r, 0] == values.cpu().numpy()[r]
 
 
+# row lengths around the kernel's 1024-element blocks: none full, one full
+# (with and without a partial tail), an odd and an even count of full blocks
 @pytest.mark.parametrize("R,V,k", [(64, 8192, 8), (37, 1000, 8), (5, 7, 8), (9, 64, 16),
-                                   (3, 1, 1), (130, 4097, 5), (2, 20000, 16)])
+                                   (3, 1, 1), (130, 4097, 5), (2, 20000, 16), (4, 1024, 16),
+                                   (7, 1500, 8), (6, 3072, 8), (5, 2048, 3)])
 def test_topk_matches_oracle(gpu_lib, R, V, k):
     vals = torch.randn(R, device=dev)
     _check_topk(_rows(R, V, torch.float32, R + V + k), k, values=vals)
