@@ -77,6 +77,7 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
   // equal to it takes the exact 64-bit test).
   uint64_t thr = 0;
   float thr_f = -__builtin_inff();
+  constexpr int kBlock = kWave * kPlyUnroll;
   // full blocks: unconditional loads at one address plus immediate offsets;
   // the last, partial block: loads masked by the row length (0 beyond it)
   auto load_full = [&](int i0, float (&v)[kPlyUnroll]) {
@@ -147,8 +148,9 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
       }
     }
     // the bound is refreshed after blocks 1, 2, 4, 8, ...: it tightens
-    // fastest early, and each refresh is a 21-stage exchange across the wave
-    const bool refresh = (nb & (nb + 1)) == 0;
+    // fastest early, and each refresh is a 21-stage exchange across the wave.
+    // None after the row's last block: only the merge follows.
+    const bool refresh = (nb & (nb + 1)) == 0 && i0 + kBlock < p.V;
     ++nb;
     if (!refresh) return;
     // bitonic sort of the lane maxima's logit keys (the upper halves; ids do
@@ -174,7 +176,6 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
   // before the current block is taken (two register buffers, alternating).
   // The full blocks' loads carry no per-lane condition, so the loads of one
   // block stay in flight while the other block is taken.
-  constexpr int kBlock = kWave * kPlyUnroll;
   const std::integral_constant<bool, true> full, first;
   const std::integral_constant<bool, false> part, rest;
   const int nfull = p.V / kBlock;
