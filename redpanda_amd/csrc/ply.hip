@@ -37,9 +37,32 @@ __device__ __forceinline__ float key_value(uint32_t k) {
   return __uint_as_float(k ^ ((k & 0x80000000u) ? 0x80000000u : 0xffffffffu));
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+// Exchanges of a 64-bit value across lanes by DPP, within rows of 16 lanes.
+template <int kCtrl>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const uint32_t lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)v, kCtrl, 0xf, 0xf, false);
+  const uint32_t hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), kCtrl, 0xf, 0xf, false);
   return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// The wave's largest value, the same in every lane: within each row of 16
+// lanes, lane i meets lane i ^ 1, i ^ 2 (quad permutes), 7 - i within its 8
+// and 15 - i within its 16 (mirrors); then the four rows' maxima are read
+// into scalars.  No LDS round trip, unlike a shuffle.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t w) {
+  w = max_u64(w, dpp_u64<0xb1>(w));   // quad_perm [1, 0, 3, 2]
+  w = max_u64(w, dpp_u64<0x4e>(w));   // quad_perm [2, 3, 0, 1]
+  w = max_u64(w, dpp_u64<0x141>(w));  // row_half_mirror
+  w = max_u64(w, dpp_u64<0x140>(w));  // row_mirror
+  uint64_t m = 0;
+#pragma unroll
+  for (int r = 0; r < kWave; r += 16) {
+    const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)w, r);
+    const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)(w >> 32), r);
+    m = max_u64(m, ((uint64_t)hi << 32) | lo);
+  }
+  return m;
 }
 
 // A logit as fp32, the storage dtype fixed at compile time (a run-time
@@ -207,12 +230,7 @@ __global__ __launch_bounds__(kThreads) void ply_topk_kernel(PlyTopkParams p) {
   float myv = -__builtin_inff();
   int myi = -1;
   for (int m = 0; m < p.k; ++m) {
-    uint64_t w = l[0];
-#pragma unroll
-    for (int s = 1; s < kWave; s <<= 1) {
-      const uint64_t o = shfl_xor_u64(w, s);
-      w = o > w ? o : w;
-    }
+    const uint64_t w = wave_max_u64(l[0]);
     if (lane == m && w != 0) {
       myv = key_value((uint32_t)(w >> 32));
       myi = (int)~(uint32_t)w;
