@@ -14,19 +14,29 @@
 // Gate arithmetic (rot_gate below).  exp uses the transcendental unit
 // (v_exp_f32: 0.8 ulp, unbiased); cos / sin do not: measured on gfx950,
 // v_cos_f32 / v_sin_f32 are off by up to ~2 ulp with a bias of +-0.3..0.6 ulp
-// that depends on the angle (-0.6 ulp near cos = 1).  That bias is a fixed
-// relative error per step, so a gate close to 1, which carries state over
-// M ~ 1/(1-g) steps, turns it into a relative drift of ~M x bias in the state
-// and in every gradient that sums over steps.  The rotational cos / sin are
-// therefore evaluated to ~1 ulp without bias: the angle in 1/256 revolutions
-// is reduced exactly to a table index plus a remainder |x| <= pi/256, where
-// cos x - 1 = -x^2/2 and sin x = x - x^3/6 are accurate to 1e-9 absolute
-// (a bias below 0.01 ulp).  (Rounding Ar*log2(e) and 256*Ai/(2 pi) once per
-// state is harmless by contrast: its error scales with dt*A, so it stays
-// ~1 ulp of the state over any memory length.)
-// The forward and the step share the gate code (cos from a per-index cubic
-// record), so the step continues the scan bit for bit; the backward
-// evaluates the same cubic from (cos, sin) pairs, to within an ulp.
+// that depends on the angle (-0.6 ulp near cos = 1).  Any error that repeats
+// at every step is a fixed relative error per step, so a gate close to 1,
+// which carries state over M ~ 1/(1-|g|) steps, turns it into a relative
+// drift of ~M x that error in the state and in every gradient summed over
+// steps.  The rotational cos / sin are therefore evaluated from an exact
+// angle reduction: the angle in 1/256 revolutions splits into a table index
+// plus a remainder |x| <= pi/256, where cos x - 1 = -x^2/2 and
+// sin x = x - x^3/6 are accurate to 1e-9 absolute.  The table records are
+// sign-folded around the nearest of +-1 (gen_sincos_table.py): a record holds
+// m = b (1 - |cos|), b = +-1 the sign of m, so the kernels form
+// w = cos / b - 1 and the gate as (b e)(1 + w) with one rounding.  |m| is
+// small where |cos| is close to 1, so the error that a table entry repeats
+// at every step that reads it stays below 0.02 ulp of the gate there (a
+// table of rounded cosines repeats up to 0.5 ulp, which drifted the A
+// gradients of long-memory states to ~2x the reference's distance from
+// float64).  The gate is then accurate to ~0.6 ulp of 1 in absolute terms,
+// which is what the state update h = g s + hb needs for any |g|.
+// (Rounding Ar*log2(e) and 256*Ai/(2 pi) once per state is harmless by
+// contrast: its error scales with dt*A, so it stays ~1 ulp of the state over
+// any memory length.)
+// The forward and the step share the gate code, so the step continues the
+// scan bit for bit; the backward evaluates the same expansion from its own
+// records (it also needs the sine), to within an ulp.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -106,8 +116,9 @@ __device__ __forceinline__ float ffma(float a, float b, float c) { return __buil
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // The gate tables copied into LDS once per workgroup (read after the
-// workgroup's next barrier): the (cos, -sin a) pairs (forward and step) or
-// the (cos, sin) pairs (backward) of the kTab table angles 2 pi k / kTab.
+// workgroup's next barrier): the sign-folded records (m, b (-sin a))
+// (forward and step) or (m, b sin) (backward) of the kTab table angles
+// 2 pi k / kTab.
 __device__ __forceinline__ void fill_cos_lin(float2* ctab, int tid) {
   for (int k = tid; k < kTab; k += kThreads) ctab[k] = kCosLin[k];
 }
@@ -193,24 +204,30 @@ __device__ __forceinline__ int angle_split(float dt, float wh, float& r) {
 // Two flavours of the same expansion, in two phases each so that a caller
 // can start the exponentials and table reads of several states before
 // finishing any of them (issue, then finish):
-//   * the forward and the step: cos as the cubic in r from the index's
-//     (c, -s a) (one 8-byte table read; the two higher coefficients one
-//     multiply each, then three FMAs);
-//   * the backward: cos and also es = 2^(dt pah) sin(a dt wh) from the
-//     index's (cos, sin) pair (one 8-byte read; the two expansions share r^2,
-//     cos - 1 and sin of the remainder).  Its gate is the forward's to
-//     within an ulp (the same cubic, rounded differently).
+//   * the forward and the step: w = cos/b - 1 as the cubic in r from the
+//     index's record (m, b (-s a)) (one 8-byte table read; the two higher
+//     coefficients one operation each, then three FMAs);
+//   * the backward: w and also b sin from the index's record (m, b s) (one
+//     8-byte read; the two expansions share r^2, cos(a r) - 1 and sin(a r)).
+//     Its gate is the forward's to within an ulp (the same expansion,
+//     rounded differently).
+// Both return the gate as (b e)(1 + w), b e = e with the sign bit of m.
 struct GatePart {
   float e;    // 2^(dt pah)
   float r;    // angle remainder, |r| <= 1/2 (table steps)
-  float2 cr;  // (c, -s a) of the table angle
+  float2 cr;  // (m, b (-s a)) of the table angle
 };
 
 struct GatePartCS {
   float e;
   float r;
-  float2 cs;  // cos, sin of the table angle
+  float2 cs;  // (m, b s) of the table angle
 };
+
+// e (>= 0) with the sign bit of m: b e for a sign-folded record.
+__device__ __forceinline__ float signed_by(float e, float m) {
+  return __uint_as_float(__float_as_uint(e) | (__float_as_uint(m) & 0x80000000u));
+}
 
 __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh, bool imag,
                                                    const float2* ctab) {
@@ -218,7 +235,7 @@ __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh
   g.e = exp2_hw(fmul(dt, pah));
   if (!imag) {
     g.r = 0.f;
-    g.cr = make_float2(1.f, 0.f);
+    g.cr = make_float2(0.f, 0.f);
     return g;
   }
   g.cr = ctab[angle_split(dt, wh, g.r)];
@@ -227,11 +244,14 @@ __device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh
 
 __device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag) {
   if (!imag) return g.e;
-  const float r = g.r;
-  // cos(a (k + r)) = c + r (-s a + r (c kC2 + r (-s a) kA3)), kA3 = -a^2/6
+  const float r = g.r, am = fabsf(g.cr.x);
+  // cos(a (k + r)) / b - 1 = -|m| + r (t + r ((1 - |m|) kC2 + r t kA3)),
+  // t = b (-s a), kA3 = -a^2/6
   constexpr float kA3 = -1.0039880779102944e-4f;
-  const float p3 = fmul(g.cr.y, kA3), p2 = fmul(g.cr.x, kC2);
-  return fmul(g.e, ffma(r, ffma(r, ffma(r, p3, p2), g.cr.y), g.cr.x));
+  const float p3 = fmul(g.cr.y, kA3), p2 = ffma(-am, kC2, kC2);
+  const float w = ffma(r, ffma(r, ffma(r, p3, p2), g.cr.y), -am);
+  const float be = signed_by(g.e, g.cr.x);
+  return ffma(be, w, be);
 }
 
 __device__ __forceinline__ GatePartCS rot_gate_issue_cs(float dt, float pah, float wh, bool imag,
@@ -240,7 +260,7 @@ __device__ __forceinline__ GatePartCS rot_gate_issue_cs(float dt, float pah, flo
   g.e = exp2_hw(fmul(dt, pah));
   if (!imag) {
     g.r = 0.f;
-    g.cs = make_float2(1.f, 0.f);
+    g.cs = make_float2(0.f, 0.f);
     return g;
   }
   g.cs = cstab[angle_split(dt, wh, g.r)];
@@ -252,14 +272,17 @@ __device__ __forceinline__ float rot_gate_finish_cs(const GatePartCS& g, bool im
     es = 0.f;
     return g.e;
   }
-  const float r = g.r;
+  const float r = g.r, am = fabsf(g.cs.x), sb = g.cs.y;  // |m|, b sin
   const float r2 = fmul(r, r);
-  const float cm1 = fmul(r2, kC2);                 // cos - 1
-  const float sx = fmul(r, ffma(r2, kS3, kS1));    // sin
-  const float cv = ffma(-g.cs.y, sx, ffma(g.cs.x, cm1, g.cs.x));
-  const float sv = ffma(g.cs.x, sx, ffma(g.cs.y, cm1, g.cs.y));
-  es = fmul(g.e, sv);
-  return fmul(g.e, cv);
+  const float cm1 = fmul(r2, kC2);                 // cos(a r) - 1
+  const float sx = fmul(r, ffma(r2, kS3, kS1));    // sin(a r)
+  // cos / b - 1 = cm1 - |m| (1 + cm1) - (b s) sin(a r)
+  const float w = ffma(-sb, sx, ffma(-am, cm1, cm1 - am));
+  // sin / b = (b s)(1 + cm1) + (1 - |m|) sin(a r)
+  const float v = ffma(sb, cm1, sb) + ffma(-am, sx, sx);
+  const float be = signed_by(g.e, g.cs.x);
+  es = fmul(be, v);
+  return ffma(be, w, be);
 }
 
 // Whether state slot j of lane slice s is rotational (n = j*S + s < NR).

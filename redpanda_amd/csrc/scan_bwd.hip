@@ -18,9 +18,9 @@
 // the backward walks chunks in reverse, recomputes the chunk's K steps into
 // registers (keeping s_{t-1}, the gate and e*sin, so the adjoint evaluates
 // no transcendental), then runs the adjoint over them.  The recompute
-// evaluates the forward's gate expansion from (cos, sin) table pairs, which
-// also give the sine (one 8-byte table read; the forward's (cos, -sin a)
-// pairs would need a second read for it); each gate matches the forward's to
+// evaluates the forward's gate expansion from (m, b sin) table records,
+// which also give the sine (one 8-byte table read; the forward's records
+// would need a second read for it); each gate matches the forward's to
 // within an ulp and every chunk restarts from the forward's checkpoint.
 //
 // Streaming: the per-step inputs (dt, (dt*u)/2, u, dy per channel; B, C per
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float sC[2][KS][NP];
   __shared__ __align__(16) float sRed[KR][2][NP][RWP];  // per-row channel sums of dB, dC
   __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
-  __shared__ float2 sCS[kTab];              // (cos, sin) pairs of the gate table
+  __shared__ float2 sCS[kTab];              // (m, b sin) records of the gate table
   // per-thread float64 sums of the parameter gradients over the batch group
   // (dA_real or dtrack, dA_imag), kept in LDS to spare registers
   __shared__ double sPar[2][NPL][kThreads];

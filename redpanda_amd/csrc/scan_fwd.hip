@@ -29,7 +29,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
   __shared__ float sY[TB][CB];     // the block's y, written out channel-contiguous
-  __shared__ float2 sCos[kTab];      // (cos, -sin a) pairs of the gate table
+  __shared__ float2 sCos[kTab];      // (m, b (-sin a)) records of the gate table
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;

@@ -44,7 +44,7 @@ __global__ __launch_bounds__(kThreads) void step_kernel(StepParams p) {
   const bool cvalid = c < p.D;
   const bool has_imag = p.Ai != nullptr;
 
-  __shared__ float2 sCos[kTab];  // (cos, -sin a) pairs of the gate table
+  __shared__ float2 sCos[kTab];  // (m, b (-sin a)) records of the gate table
   fill_cos_lin(sCos, tid);
   GateRegs<NPL> gp;
   float h[NPL], hbp[NPL], Bs[NPL], Cs[NPL];
@@ -165,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
   constexpr int TCH = kStepTile;
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
-  __shared__ float2 sCos[kTab];           // (cos, -sin a) pairs of the gate table
+  __shared__ float2 sCos[kTab];           // (m, b (-sin a)) records of the gate table
   __shared__ float sBC[kStepRiMax][NBC * NP];  // B, C (B_prev) rows of the workgroup's rollouts
   // the (h, beta) block of one rollout: TCH channels x NP states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NV
