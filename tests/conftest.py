@@ -33,3 +33,22 @@ def gpu_lib():
     if not torch.cuda.is_available():
         pytest.fail("GPU test collected on a host without a GPU")
     return _lib.load()
+
+
+@pytest.hookimpl(trylast=True)
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """One line per parity test (its worst figures), recorded by the tests
+    through record_property("parity", ...), printed even under -q so that
+    a run's log carries the numbers and not only the pass count."""
+    lines = []
+    for key in ("passed", "failed"):
+        for rep in terminalreporter.stats.get(key, []):
+            if getattr(rep, "when", "call") != "call":
+                continue
+            for name, value in getattr(rep, "user_properties", ()):
+                if name == "parity":
+                    lines.append(("" if key == "passed" else "FAILED ") + str(value))
+    if lines:
+        terminalreporter.write_sep("-", "parity figures (max|a-b|/max|b| per tensor)")
+        for line in lines:
+            terminalreporter.write_line(line)

@@ -46,7 +46,8 @@ def _inputs(lead, N, P, dt, seed, dt_rank=7):
 
 
 def nrel(a, b):
-    return float((a.float() - b.float()).abs().max() / (b.float().abs().max() + 1e-30))
+    a, b = a.detach().float(), b.detach().float()
+    return float((a - b).abs().max() / (b.abs().max() + 1e-30))
 
 
 CASES = [((2, 64), 40, 4), ((3, 17), 20, 4), ((5,), 1, 1), ((2, 9), 64, 2), ((1, 33), 65, 3),

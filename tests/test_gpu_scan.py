@@ -150,7 +150,7 @@ def within_bar(e_hip_ref, e_hip_64, e_ref_64, tol):
     return e_hip_ref <= tol or e_hip_64 <= max(tol, e_ref_64)
 
 
-def compare(c, bidirectional, tag, grad_tol=GRAD_TOL):
+def compare(c, bidirectional, tag, grad_tol=GRAD_TOL, record=None):
     y, g = hip_run(c, bidirectional)
     y32, g32 = oracle_fp32(c, bidirectional)
     y64, g64 = oracle_fp64(c, bidirectional)
@@ -161,6 +161,12 @@ def compare(c, bidirectional, tag, grad_tol=GRAD_TOL):
         rep[k] = (rel(g[k], g32[k]), rel(g[k], g64[k]), rel(g32[k], g64[k]))
     print(tag, " ".join("%s[%.1e %.1e %.1e]" % (k, *v) for k, v in rep.items()),
           "(hip-ref hip-f64 ref-f64)", flush=True)
+    if record is not None:
+        g = {k: v for k, v in rep.items() if k != "y"}
+        wk = max(g, key=lambda k: g[k][0])
+        record("parity", f"scan {tag}: y hip-ref {rep['y'][0]:.1e} (hip-f64 {rep['y'][1]:.1e}, "
+                         f"ref-f64 {rep['y'][2]:.1e}); worst grad hip-ref {g[wk][0]:.1e} ({wk}; "
+                         f"hip-f64 {g[wk][1]:.1e}, ref-f64 {g[wk][2]:.1e})")
     assert within_bar(*rep.pop("y"), FWD_TOL), tag
     for k, v in rep.items():
         assert within_bar(*v, grad_tol), f"{tag}: grad {k} (hip-ref, hip-f64, ref-f64) = {v}"
@@ -210,16 +216,16 @@ def test_mixed_input_dtypes(gpu_lib):
     compare(c, False, "mixed dtypes")
 
 
-def test_eval_mamba_shape_reduced_batch(gpu_lib):
+def test_eval_mamba_shape_reduced_batch(gpu_lib, record_property):
     """C2/C3 shape (D=1536, N=40 = 32 rot + 8 track, L=64, bf16 storage) at B=2."""
     c = make_case(1002, B=2, L=64, D=1536, NR=32, NT=8, dtype=torch.bfloat16)
-    compare(c, True, "eval-mamba bidir B=2")
+    compare(c, True, "eval-mamba bidir B=2", record=record_property)
 
 
-def test_long_sequence_reduced(gpu_lib):
+def test_long_sequence_reduced(gpu_lib, record_property):
     """C5 shape per channel (L=2048, N=72 = 64 rot + 8 track) at B=1, D=64."""
     c = make_case(1005, B=1, L=2048, D=64, NR=64, NT=8)
-    compare(c, False, "long L=2048")
+    compare(c, False, "long L=2048", record=record_property)
 
 
 def test_autograd_wrapper_dtype_contract(gpu_lib):

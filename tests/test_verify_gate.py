@@ -55,6 +55,87 @@ def test_gate_refuses_planted_errors(y_err, g_err, needle):
         gate.check_gate(_errs(y_err, g_err))
 
 
+def _oracle_case(planted=None):
+    """The gate's comparison run on the CPU with the oracle's fp32
+    restatement of the reference model standing in for the product:
+    (errors of the fp32 run, errors of the fp32 run with `planted` applied).
+    planted: "trapezoid" drops the 1/2 g beta_prev term of every scan token
+    (engine/mamba.py:409-412), "grad" scales one gradient by 1 + 3e-4."""
+    from oracle import model_ref
+    torch.manual_seed(4)
+    cfg = model_ref.MambaConfig(d_model=16, n_layer=2, d_state=8, n_track_state=2, mimo_p=2,
+                                vocab_size=64, bidirectional=True)
+    m = model_ref.Mamba(cfg)
+    with torch.no_grad():
+        gen = torch.Generator().manual_seed(5)
+        for layer in m.layers:
+            layer["mixer"].A_phase.copy_((torch.rand(layer["mixer"].A_phase.shape, generator=gen) * 2 - 1) * 1.4)
+    m.train()
+    ids = torch.randint(0, 64, (2, 33), generator=torch.Generator().manual_seed(6))
+    proj = torch.randn(2, 33, 16, generator=torch.Generator().manual_seed(7))
+    params64 = {k: v.detach().double().requires_grad_(True) for k, v in m.named_parameters()}
+    y64 = gate._model64(m, ids, params64)
+    (y64 * proj.double()).sum().backward()
+    g64 = {k: v.grad for k, v in params64.items()}
+
+    def fp32_run():
+        m.zero_grad(set_to_none=True)
+        y = m(ids)
+        (y * proj).sum().backward()
+        return y.detach(), {k: p.grad.clone() for k, p in m.named_parameters()}
+
+    y, grads = fp32_run()
+    clean = gate.gate_errors(y, y64.detach(), grads, g64)
+    if planted == "trapezoid":
+        orig = scan_ref.scan_chunk_ref
+
+        def dropped(delta_c, u_c, B_c, C_c, h, beta_prev, A_real, A_imag, track):
+            # the planted mistake: tokens without the 1/2 g beta_{t-1} term
+            gates = scan_ref.gate_tensor_ref(delta_c, A_real, A_imag, track)
+            beta = torch.einsum("bld,bln->bldn", delta_c, B_c) * u_c.unsqueeze(-1)
+            tokens = 0.5 * beta
+            first = tokens[:, 0] + gates[:, 0] * h.to(gates.dtype)
+            tokens = torch.cat([first.unsqueeze(1), tokens[:, 1:]], dim=1)
+            hs = scan_ref.hillis_steele_scan(gates, tokens)
+            return torch.einsum("bldn,bln->bld", hs, C_c), hs[:, -1], beta[:, -1]
+        scan_ref.scan_chunk_ref = dropped
+        try:
+            y, grads = fp32_run()
+        finally:
+            scan_ref.scan_chunk_ref = orig
+    elif planted == "grad":
+        grads = dict(grads)
+        grads["layers.0.mixer.A_phase"] = grads["layers.0.mixer.A_phase"] * (1 + 3e-4)
+    return clean, gate.gate_errors(y, y64.detach(), grads, g64)
+
+
+def test_gate_passes_the_reference_algorithm():
+    """The reference's own fp32 algorithm (the oracle) passes the gate."""
+    clean, _ = _oracle_case()
+    gate.check_gate(clean)
+
+
+@pytest.mark.parametrize("planted,needle", [("trapezoid", "mismatch"),
+                                            ("grad", "grad mismatch \\(norm-wise\\)")])
+def test_gate_refuses_a_planted_model_error(planted, needle):
+    """A whole model's results with a planted mistake (a dropped trapezoid
+    term in every scan; one parameter gradient 3e-4 off) are refused."""
+    _, bad = _oracle_case(planted)
+    with pytest.raises(AssertionError, match=needle):
+        gate.check_gate(bad)
+
+
 @pytest.mark.gpu
 def test_hip_path_passes_the_gate(gpu_lib):
     assert gate.verify("cuda", thorough=False, verbose=True)
+
+
+@pytest.mark.gpu
+def test_hip_path_passes_the_thorough_gate(gpu_lib, record_property):
+    """The reference gate's full matrix (engine/triton_scan.py:353-357):
+    d_model 512 with d_state 64 of which 16 tracking and mimo_p 4 beside the
+    two small configurations, L in {1, 31, 32, 33, 70, 107, 160}, both
+    directions."""
+    assert gate.verify("cuda", thorough=True, verbose=True)
+    record_property("parity", "gate verify(thorough=True): 42 cases within 2e-3 (reference "
+                              "criteria) and 1e-4 norm-wise of float64")
