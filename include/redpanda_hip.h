@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 10
+#define RP_ABI_VERSION 11
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -383,6 +383,27 @@ int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream)
  * sums and the dA atomics, here as deterministic two-stage reductions.
  */
 int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream);
+
+/*
+ * rp_scan_bwd without a caller workspace: the same kernels, with their
+ * scratch (the per-tile dB / dC partials and the per-batch-group parameter
+ * gradient partials) in a static device array of RP_SCAN_BWD_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It allocates nothing and frees nothing; io->work and
+ * io->work_bytes are ignored.  A shape whose rp_scan_bwd_work_bytes()
+ * exceeds the scratch is refused with RP_ERR_WORKSPACE (for example the
+ * Eval-Mamba layer, d_inner 1536 and d_state 40 at L = 64, fits up to about
+ * 50 batch rows).  Every call on one GPU shares that GPU's scratch, which
+ * keeps the last call's contents: calls that overlap on one GPU (concurrent
+ * streams, host threads, parallel graph branches) race and must be
+ * serialised.  Every partial is written before it is read, so nothing needs
+ * clearing between calls.  The scratch is looked up on the stream's device
+ * on the first call there.
+ */
+#define RP_SCAN_BWD_SCRATCH_BYTES (64ll << 20)
+int rp_scan_bwd_noalloc(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream);
 
 /* Validate step arguments on the host without launching anything. */
 int rp_step_check(const rp_step_args* a);

@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -126,6 +126,8 @@ SIGNATURES = {
     "rp_scan_bwd_work_bytes": (_i64, [ctypes.POINTER(ScanArgs)]),
     "rp_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanFwdOut), _vp]),
     "rp_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBwdIO), _vp]),
+    "rp_scan_bwd_noalloc": (ctypes.c_int, [ctypes.POINTER(ScanArgs), ctypes.POINTER(ScanBwdIO),
+                                           _vp]),
     "rp_step_check": (ctypes.c_int, [ctypes.POINTER(StepArgs)]),
     "rp_step": (ctypes.c_int, [ctypes.POINTER(StepArgs), _vp]),
     "rp_bcnorm_check": (ctypes.c_int, [ctypes.POINTER(BcNormArgs)]),

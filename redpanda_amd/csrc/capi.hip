@@ -4,6 +4,8 @@
 // message (rp_last_error).
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -289,7 +291,58 @@ int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream)
   return RP_OK;
 }
 
-int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
+}  // extern "C"
+
+// Scratch of rp_scan_bwd_noalloc: one static device array, each GPU holding
+// its own copy at its own address for as long as the process runs.  Host code
+// uses the array only to look that address up (hipGetSymbolAddress, once per
+// device); everything else goes through the looked-up device pointer.
+static __device__ __align__(256) unsigned char scratch[RP_SCAN_BWD_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the device that `stream` runs on.
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return fail_hip(e, "scan bwd noalloc: hipGetDevice");
+  int dev = cur;
+  if (stream != nullptr) {
+    hipDevice_t sd = 0;
+    e = hipStreamGetDevice(stream, &sd);
+    if (e != hipSuccess) return fail_hip(e, "scan bwd noalloc: hipStreamGetDevice");
+    dev = (int)sd;
+  }
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(RP_ERR_UNSUPPORTED, "scan bwd noalloc: device %d beyond %d", dev, kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      // with the stream's device current, as the lookup is per device
+      if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+        return fail_hip(e, "scan bwd noalloc: hipSetDevice");
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      hipError_t e2 = dev != cur ? hipSetDevice(cur) : hipSuccess;
+      if (e != hipSuccess) return fail_hip(e, "scan bwd noalloc: hipGetSymbolAddress(scratch)");
+      if (e2 != hipSuccess) return fail_hip(e2, "scan bwd noalloc: hipSetDevice (restore)");
+      if (p == nullptr) return fail(RP_ERR_LAUNCH, "scan bwd noalloc: scratch has no address");
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return RP_OK;
+}
+
+// rp_scan_bwd with its scratch given: the caller's workspace (use_io_work)
+// or the static scratch of rp_scan_bwd_noalloc.
+int scan_bwd_impl(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream,
+                  bool use_io_work) {
   int st = scan_validate(a);
   if (st != RP_OK) return st;
   if (io == nullptr) return fail(RP_ERR_INVALID, "scan bwd: NULL io block");
@@ -318,9 +371,21 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
     return fail(RP_ERR_INVALID, "scan bwd: d_h0 needs an initial state h0");
   if ((io->dh_last || io->dbeta_last) && a->bidirectional)
     return fail(RP_ERR_INVALID, "scan bwd: final-state gradients exist for causal scans only");
-  if (need > 0 && (io->work == nullptr || io->work_bytes < need || !aligned(io->work, 256)))
-    return fail(RP_ERR_WORKSPACE, "scan bwd: workspace needs %lld bytes (256-aligned), got %lld",
-                (long long)need, (long long)io->work_bytes);
+  void* scr = nullptr;
+  if (use_io_work) {
+    if (need > 0 && (io->work == nullptr || io->work_bytes < need || !aligned(io->work, 256)))
+      return fail(RP_ERR_WORKSPACE, "scan bwd: workspace needs %lld bytes (256-aligned), got %lld",
+                  (long long)need, (long long)io->work_bytes);
+    scr = io->work;
+  } else if (need > 0) {
+    if (need > RP_SCAN_BWD_SCRATCH_BYTES)
+      return fail(RP_ERR_WORKSPACE,
+                  "scan bwd noalloc: this shape needs %lld bytes of scratch, the static scratch "
+                  "holds %lld; use rp_scan_bwd with a workspace of rp_scan_bwd_work_bytes()",
+                  (long long)need, (long long)RP_SCAN_BWD_SCRATCH_BYTES);
+    st = scratch_for_stream((hipStream_t)stream, &scr);
+    if (st != RP_OK) return st;
+  }
   if (a->D == 0) return RP_OK;
   if ((int64_t)pl.ntiles * pl.nbg > kI32Max)
     return fail(RP_ERR_UNSUPPORTED, "scan bwd: grid too large");
@@ -338,8 +403,8 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
   b.d_beta0 = io->d_beta0;
   b.d_delta = io->d_delta;
   b.d_u = io->d_u;
-  b.part_bc = static_cast<float*>(io->work);
-  b.part_par = reinterpret_cast<double*>(static_cast<char*>(io->work) + pl.part_bc_bytes);
+  b.part_bc = static_cast<float*>(scr);
+  b.part_par = reinterpret_cast<double*>(static_cast<char*>(scr) + pl.part_bc_bytes);
   b.bg = pl.bg;
   b.nbg = pl.nbg;
   hipStream_t s = (hipStream_t)stream;
@@ -353,6 +418,18 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
                                          a->NT > 0 ? io->d_track : nullptr, s);
   if (e != hipSuccess) return fail_hip(e, "scan bwd finalize launch");
   return RP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
+  return scan_bwd_impl(a, io, stream, true);
+}
+
+int rp_scan_bwd_noalloc(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream) {
+  return scan_bwd_impl(a, io, stream, false);
 }
 
 int rp_step_check(const rp_step_args* a) {
