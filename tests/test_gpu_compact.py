@@ -134,7 +134,8 @@ def test_training_through_compact_step(gpu_lib):
             x, cache = m.step(token_id=toks[:, t], cache=cache)
             loss = loss + x.square().mean()
         loss.backward()
-        return float(loss), {k: p.grad.clone() for k, p in m.named_parameters() if p.grad is not None}
+        return float(loss.detach()), {k: p.grad.clone() for k, p in m.named_parameters()
+                                      if p.grad is not None}
 
     l0, g0 = run(False)
     l1, g1 = run(True)
