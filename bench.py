@@ -18,7 +18,10 @@ Besides the headline number the JSON line carries:
                 scan being VALU-bound) its vector-ALU issue rate against
                 the VALU peak;
   kernels       the same for every kernel of the path;
-  long_sequence tokens/s of a causal fwd + bwd at L=2048, d_state 72;
+  long_sequence tokens/s of a causal fwd + bwd at L=2048, d_state 72, with
+                each kernel's HBM and VALU roofline (profiles/*_long.json);
+  c1            the reference's CPU configuration (causal real-decay forward,
+                B=8 L=64 D=256 N=16) on the GPU, beside its CPU baseline;
   step          rollout-steps/s of the fused step kernel over 8 layers;
   layer         tokens/s of a whole bidirectional Mamba3Block fwd + bwd, fused,
                 beside the reference's layer with only its scan swapped;
@@ -28,7 +31,9 @@ Besides the headline number the JSON line carries:
                 pinned boundary (one upload, the top-k kernel, one download)
                 beside the reference's per-rollout reads, sampled;
   cpu_baseline  the reference's CPU PyTorch path (the oracle's fp32
-                restatement) on a bounded sample, on this host's cores.
+                restatement) on a bounded sample, on this host's cores;
+                the step, layer, C1 and long-sequence blocks carry their
+                own.
 Only one GPU is used; --gpus above 1 exits with a message.
 """
 
@@ -60,6 +65,9 @@ STEP_SHAPE = dict(R=4096, layers=8, D=1024, NR=16, NT=4)
 # Long-sequence causal stress: batch 64, L=2048, d_inner 1024, d_state 64
 # complex plus 8 tracking, fp32 inputs.
 LONG_SHAPE = dict(B=64, L=2048, D=1024, NR=64, NT=8)
+# The reference's CPU configuration: one causal layer, batch 8, L=64, 8 heads
+# x head_dim 32 (d_inner 256), d_state 16 real decay-only, forward only.
+C1_SHAPE = dict(B=8, L=64, D=256, NR=16, NT=0)
 
 
 def parse():
@@ -80,6 +88,9 @@ def parse():
                     help="counter pass: run each kernel of the path a few times at the bench "
                          "shapes plus one elementwise pass over 1 GiB (torch.neg: the reference "
                          "dispatch that scales FETCH_SIZE / WRITE_SIZE), then exit")
+    ap.add_argument("--profile-pass-long", action="store_true",
+                    help="the same counter pass for the long-sequence scan kernels only (their "
+                         "dB / dC reduction shares its name with the Eval-shape one)")
     return ap.parse_args()
 
 
@@ -642,9 +653,9 @@ def bench_layer(torch, args):
     return dict(t_fused=t_fused, t_dropin=t_dropin, tok_fused=T / t_fused, tok_dropin=T / t_dropin)
 
 
-def bench_long(torch, args):
-    """Causal fwd + bwd at the long-sequence shape, through the C ABI with
-    preallocated buffers (inputs generated on the device)."""
+def long_setup(torch):
+    """Device inputs and preallocated buffers of the long-sequence shape
+    (generated on the device), and fwd() / bwd() calls through the C ABI."""
     from redpanda_amd import _lib
     from redpanda_amd.scan import make_scan_args
     import torch.nn.functional as F
@@ -679,6 +690,7 @@ def bench_long(torch, args):
                         d_A_real=g[4].data_ptr(), d_A_imag=g[5].data_ptr(),
                         d_track=g[6].data_ptr(), work=work.data_ptr(), work_bytes=work.numel())
     stream = _lib.stream_of(dev)
+    keep = (u, dt, Bc, Cc, Ar, Ai, Tk, dy, y, ckpt, g, work, a, out, io)
 
     def fwd():
         _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out), stream), lib)
@@ -686,6 +698,15 @@ def bench_long(torch, args):
     def bwd():
         _lib.check(lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), stream), lib)
 
+    return fwd, bwd, keep
+
+
+def bench_long(torch, args):
+    """Causal fwd + bwd at the long-sequence shape, through the C ABI with
+    preallocated buffers (inputs generated on the device)."""
+    sh = LONG_SHAPE
+    B, L, D, NR, NT = sh["B"], sh["L"], sh["D"], sh["NR"], sh["NT"]
+    fwd, bwd, keep = long_setup(torch)
     fwd()
     bwd()
     torch.cuda.synchronize()
@@ -693,15 +714,59 @@ def bench_long(torch, args):
     reps = max(2, min(args.steps, 5))
     t_f = timer.time(fwd, reps)
     t_b = timer.time(bwd, reps)
-    fb, bb = scan_bytes(B, L, D, N, NR, NT, 4, False)
+    fb, bb = scan_bytes(B, L, D, NR + NT, NR, NT, 4, False)
+    del keep
     return dict(tok_s=B * L / (t_f + t_b), t_fwd=t_f, t_bwd=t_b, fwd_bytes=fb, bwd_bytes=bb)
 
 
-def measured_valu():
-    """VALU wave-instructions per launch from the committed counter summary
+def bench_c1(torch, args):
+    """The reference's CPU configuration on the GPU: one causal real-decay
+    scan forward (fp32 inputs, no checkpoints), per launch."""
+    from redpanda_amd import _lib
+    from redpanda_amd.scan import make_scan_args
+    sh = C1_SHAPE
+    B, L, D, NR = sh["B"], sh["L"], sh["D"], sh["NR"]
+    c = c1_inputs(torch, "cuda:0")
+    lib = _lib.load()
+    a = make_scan_args(c["delta"], c["u"], c["Bc"], c["Cc"], c["Ar"], None, None, False)
+    y = torch.empty((B, L, D), dtype=torch.float32, device="cuda:0")
+    out = _lib.ScanFwdOut(y.data_ptr(), None, None, None)
+    stream = _lib.stream_of(torch.device("cuda:0"))
+
+    def fwd():
+        _lib.check(lib.rp_scan_fwd(ctypes.byref(a), ctypes.byref(out), stream), lib)
+
+    for _ in range(3):
+        fwd()
+    torch.cuda.synchronize()
+    t = EventTimer(torch).time(fwd, max(20, args.steps))
+    fb, _ = scan_bytes(B, L, D, NR, NR, 0, 4, False)
+    return dict(tok_s=B * L / t, t_fwd=t, fwd_bytes=fb)
+
+
+def c1_inputs(torch, device):
+    """C1's inputs: x ~ N(0,1); dt = softplus(N(-2,0.5)); A = -exp(U(log 1,
+    log 16)); B and C ~ N(0,1), RMS-normalised per token (fp32)."""
+    import torch.nn.functional as F
+    sh = C1_SHAPE
+    B, L, D, NR = sh["B"], sh["L"], sh["D"], sh["NR"]
+    gen = torch.Generator().manual_seed(1001)
+    u = torch.randn(B, L, D, generator=gen)
+    dt = F.softplus(torch.randn(B, L, D, generator=gen) * 0.5 - 2.0)
+    Bc = torch.randn(B, L, NR, generator=gen)
+    Cc = torch.randn(B, L, NR, generator=gen)
+    Bc = Bc / Bc.pow(2).mean(-1, keepdim=True).sqrt()
+    Cc = Cc / Cc.pow(2).mean(-1, keepdim=True).sqrt()
+    Ar = -torch.exp(torch.rand(D, NR, generator=gen) * math.log(16.0))
+    return {k: v.to(device) for k, v in dict(delta=dt, u=u, Bc=Bc, Cc=Cc, Ar=Ar).items()}
+
+
+def measured_valu(name="valu.json"):
+    """VALU wave-instructions per launch from a committed counter summary
     (profiles/valu.json, written by `python -m redpanda_amd.profiling valu`
-    from an SQ_INSTS_VALU pass over `bench.py --profile-pass`), or {}."""
-    path = os.path.join(ROOT, "profiles", "valu.json")
+    from an SQ_INSTS_VALU pass over `bench.py --profile-pass`;
+    profiles/valu_long.json from `--profile-pass-long`), or {}."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as fh:
             k = json.load(fh)["kernels"]
@@ -719,12 +784,13 @@ def valu_roofline(instr, seconds):
             "instructions_per_launch": instr}
 
 
-def measured_traffic():
-    """HBM bytes per launch from the committed counter summary
+def measured_traffic(name="traffic.json"):
+    """HBM bytes per launch from a committed counter summary
     (profiles/traffic.json, written by `python -m redpanda_amd.profiling
     traffic` from FETCH_SIZE / WRITE_SIZE passes over `bench.py
-    --profile-pass`), or {} when there is none."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+    --profile-pass`; profiles/traffic_long.json from `--profile-pass-long`),
+    or {} when there is none."""
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as fh:
             k = json.load(fh)["kernels"]
@@ -832,6 +898,119 @@ def profile_pass(torch):
           f"calibration neg {src.numel() * 4} bytes each way", file=sys.stderr, flush=True)
 
 
+def profile_pass_long(torch):
+    """The long-sequence scan kernels, three dispatches each way, then the
+    1 GiB calibration dispatch, for counter runs of their own."""
+    fwd, bwd, keep = long_setup(torch)
+    for _ in range(3):
+        fwd()
+        bwd()
+    torch.cuda.synchronize()
+    del keep
+    dev = torch.device("cuda:0")
+    src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("[bench] long-sequence profile pass done: scan fwd/bwd x3, calibration neg "
+          f"{src.numel() * 4} bytes each way", file=sys.stderr, flush=True)
+
+
+def _host_info():
+    import torch
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": cpu_model, "os_cpu_count": os.cpu_count(), "torch": torch.__version__}
+
+
+def _median_time(run, budget_s, min_runs, max_runs, warm=2):
+    for _ in range(warm):
+        run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and
+                                    len(times) < max_runs):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * budget_s:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_c1_baseline(budget_s):
+    """C1 in full on the CPU: the reference's fp32 chunk-streaming scan
+    (the oracle's restatement of engine/mamba.py:318-423), forward only."""
+    import torch
+    from oracle import scan_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    sh = C1_SHAPE
+    c = c1_inputs(torch, "cpu")
+
+    def run():
+        with torch.no_grad():
+            scan_ref.contracted_scan_ref(c["delta"], c["u"], c["Bc"], c["Cc"], c["Ar"], None,
+                                         None, sh["NR"])
+
+    med, n = _median_time(run, budget_s, 5, 50)
+    return {"value": sh["B"] * sh["L"] / med, "unit": "tokens/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"the whole configuration: oracle fp32 restatement of the reference CPU "
+                       f"scan, causal real decay, forward, B={sh['B']} L={sh['L']} D={sh['D']} "
+                       f"N={sh['NR']}; median of {n} runs"), **_host_info()}
+
+
+def cpu_long_baseline(budget_s):
+    """The long-sequence layer on the CPU: the oracle's fp32 restatement of
+    the reference's chunk-streaming scan with per-chunk checkpointing,
+    causal, forward + autograd backward, at batch 1 and a quarter of the
+    channels; channels are independent and the work is linear in them, so
+    tokens/s is scaled to the full width."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import scan_ref
+    torch.set_num_threads(os.cpu_count() or 1)
+    sh = LONG_SHAPE
+    Bs, Ds = 1, sh["D"] // 4
+    L, NR, NT = sh["L"], sh["NR"], sh["NT"]
+    N = NR + NT
+    gen = torch.Generator().manual_seed(1005)
+    u = torch.randn(Bs, L, Ds, generator=gen)
+    dt = F.softplus(torch.randn(Bs, L, Ds, generator=gen) * 0.5 - 2.0)
+    Bc = torch.randn(Bs, L, N, generator=gen)
+    Cc = torch.randn(Bs, L, N, generator=gen)
+    Bc = Bc / Bc.pow(2).mean(-1, keepdim=True).sqrt()
+    Cc = Cc / Cc.pow(2).mean(-1, keepdim=True).sqrt()
+    Ar = -torch.exp(torch.rand(Ds, NR, generator=gen) * 3.0)
+    Ai = (torch.rand(Ds, NR, generator=gen) * 2 - 1) * math.pi
+    Tk = torch.tanh(torch.randn(Ds, NT, generator=gen) * 1.5)
+    dy = torch.randn(Bs, L, Ds, generator=gen)
+    args = (dt, u, Bc, Cc, Ar, Ai, Tk)
+
+    def run():
+        lv = [t.clone().requires_grad_(True) for t in args]
+        y, _ = scan_ref.contracted_scan_ref(*lv, N, checkpoint=True)
+        (y * dy).sum().backward()
+
+    med, n = _median_time(run, budget_s, 3, 20, warm=1)
+    scale = Ds / sh["D"]
+    return {"value": Bs * L / med * scale, "unit": "tokens/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"oracle fp32 restatement of the reference CPU scan (chunk-streaming "
+                       f"Hillis-Steele, per-chunk checkpoint), causal fwd+bwd, B={Bs} L={L} "
+                       f"D={Ds} of {sh['D']} N={N}; median of {n} runs, tokens/s scaled by "
+                       f"{Ds}/{sh['D']} (the work is linear in the independent channels)"),
+            **_host_info()}
+
+
 def cpu_baseline(budget_s):
     """The reference's CPU PyTorch path: the fp32 chunk-streaming Hillis-Steele
     scan with per-chunk checkpointing (engine/mamba.py:318-423), both
@@ -931,7 +1110,7 @@ def cpu_step_baseline(budget_s):
     from oracle import scan_ref
     torch.set_num_threads(os.cpu_count() or 1)
     sh = STEP_SHAPE
-    R, D, NR, NT = 256, sh["D"], sh["NR"], sh["NT"]
+    R, D, NR, NT = sh["R"], sh["D"], sh["NR"], sh["NT"]
     N = NR + NT
     gen = torch.Generator().manual_seed(1004)
     layers = []
@@ -953,14 +1132,16 @@ def cpu_step_baseline(budget_s):
 
     ply()
     plies, t0 = 0, time.perf_counter()
-    while plies < 3 or (time.perf_counter() - t0 < budget_s and plies < 50):
+    while plies < 2 or (time.perf_counter() - t0 < budget_s and plies < 32):
         ply()
         plies += 1
     el = time.perf_counter() - t0
     return {"value": R * plies / el, "unit": "rollout-steps/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": (f"oracle fp32 restatement of the reference torch step (SSM core), "
-                       f"{sh['layers']} layers, R={R} rollouts, D={D} N={N}, {plies} plies")}
+                       f"{sh['layers']} layers, R={R} rollouts, D={D} N={N}: {plies} of the "
+                       f"32 plies after one warm-up ply (a ply costs the same at any depth: "
+                       f"the state is O(1))"), **_host_info()}
 
 
 def main():
@@ -976,6 +1157,9 @@ def main():
         sys.exit(1)
     if args.profile_pass:
         profile_pass(torch)
+        return
+    if args.profile_pass_long:
+        profile_pass_long(torch)
         return
     print(f"[bench] scan fwd+bwd {SCAN_SHAPE} bf16 storage, steps={args.steps} "
           f"warmup={args.warmup}", file=sys.stderr, flush=True)
@@ -997,6 +1181,9 @@ def main():
         lng = bench_long(torch, args)
         print(f"[bench] long: {lng['tok_s']:.4g} tokens/s; fwd {lng['t_fwd'] * 1e3:.2f} ms, "
               f"bwd {lng['t_bwd'] * 1e3:.2f} ms", file=sys.stderr, flush=True)
+    c1 = bench_c1(torch, args)
+    print(f"[bench] C1 (B=8 L=64 D=256 N=16 real, causal fwd): {c1['tok_s']:.4g} tokens/s, "
+          f"{c1['t_fwd'] * 1e6:.1f} us/launch", file=sys.stderr, flush=True)
     ply = None
     if not args.no_step:
         ply = bench_ply(torch, args)
@@ -1039,8 +1226,15 @@ def main():
             print(f"[bench] cpu layer: {lay['cpu_baseline']['value']:.4g} tokens/s",
                   file=sys.stderr, flush=True)
         if step is not None:
-            step["cpu_baseline"] = cpu_step_baseline(args.cpu_seconds / 3)
+            step["cpu_baseline"] = cpu_step_baseline(args.cpu_seconds / 2)
             print(f"[bench] cpu step: {step['cpu_baseline']['value']:.4g} rollout-steps/s",
+                  file=sys.stderr, flush=True)
+        c1["cpu_baseline"] = cpu_c1_baseline(args.cpu_seconds / 5)
+        print(f"[bench] cpu C1: {c1['cpu_baseline']['value']:.4g} tokens/s", file=sys.stderr,
+              flush=True)
+        if lng is not None:
+            lng["cpu_baseline"] = cpu_long_baseline(args.cpu_seconds / 3)
+            print(f"[bench] cpu long: {lng['cpu_baseline']['value']:.4g} tokens/s",
                   file=sys.stderr, flush=True)
 
     # dominant kernel: the longer of forward (training) and backward
@@ -1112,13 +1306,33 @@ def main():
                 "achieved_GBps": step["GBps_shared"]},
         }
     if lng is not None:
+        trl, vcl = measured_traffic("traffic_long.json"), measured_valu("valu_long.json")
+
+        def lk(kernel, key, secs, nbytes):
+            gbs = nbytes / secs / 1e9
+            return {"kernel": kernel, "avg_launch_s": secs, "alg_bytes_per_launch": nbytes,
+                    "hbm": {"achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": gbs / HBM_PEAK_GBS, "traffic": trl.get(key)},
+                    "valu": valu_roofline(vcl.get(key.split("+")[0]), secs)}
         line["long_sequence"] = {
             "metric": "tokens/s", "value": lng["tok_s"],
             "config": {"workload": "causal trapezoidal scan layer, fwd+bwd, fp32 inputs",
                        **LONG_SHAPE, "d_state": LONG_SHAPE["NR"] + LONG_SHAPE["NT"]},
             "fwd_s": lng["t_fwd"], "bwd_s": lng["t_bwd"],
             "alg_bytes_fwd": lng["fwd_bytes"], "alg_bytes_bwd": lng["bwd_bytes"],
+            "roofline": [lk("scan_fwd_kernel (causal, checkpoints)", "scan_fwd_kernel",
+                            lng["t_fwd"], lng["fwd_bytes"]),
+                         lk("scan_bwd_kernel + reductions", "scan_bwd_kernel+reductions",
+                            lng["t_bwd"], lng["bwd_bytes"])],
+            "cpu_baseline": lng.get("cpu_baseline"),
         }
+    line["c1"] = {
+        "metric": "tokens/s", "value": c1["tok_s"],
+        "config": {"workload": "the reference's CPU configuration: one causal real-decay scan "
+                               "layer forward, fp32", **C1_SHAPE, "d_state": C1_SHAPE["NR"]},
+        "avg_launch_s": c1["t_fwd"], "alg_bytes_per_launch": c1["fwd_bytes"],
+        "cpu_baseline": c1.get("cpu_baseline"),
+    }
     if lay is not None:
         line["layer"] = {
             "metric": "tokens/s", "value": lay["tok_fused"],

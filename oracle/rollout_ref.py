@@ -11,29 +11,51 @@ in numpy, what the reference computes on the host from each rollout's rows:
   select_move(...)         the policy-guided walk over the candidates
                            (:266-276), greedy or a softmax draw
 
-Tie order: the reference's argsort is not stable, so equal logits come in
-an unspecified order there; `candidates` orders them by ascending token id,
-the order the device kernel documents, and tests of ties use that rule.
+Order: numpy's, as the reference's argpartition / argsort apply it: -0 and
++0 are equal and every NaN is above +inf whatever its sign.  The
+reference's argsort is not stable, so equal logits come in an unspecified
+order there; `candidates` orders them by ascending token id, the order the
+device kernel documents, and tests of ties use that rule.  The returned
+logits are the canonical values (+0.0 for -0.0, a NaN with its sign bit
+cleared), equal in value to the reference's `float(ln[mid])`; NaNs with
+different payloads are ordered by payload, which numpy leaves unspecified
+(a canonical NaN has one payload).
 
 Parity pins (tests/test_oracle.py): `candidates` against a full stable sort
-by (-logit, id), the brute force for tiny rows; against the reference's own
-argpartition/argsort expression on tie-free rows; and the set property (no
-logit outside the list exceeds one inside it).  `gather_legal` against
-direct indexing.  `select_move` against the reference's walk restated on
-python-level mocks (greedy = first legal candidate; the draw uses the same
-RNG call sequence).
+by (-logit, id), the brute force for tiny rows (with +-0, +-inf and NaNs of
+both signs); against the reference's own argpartition/argsort expression on
+tie-free rows, NaNs included; and the set property (no logit outside the
+list exceeds one inside it).  `gather_legal` against direct indexing.
+`select_move`: greedy = the first legal candidate; the draw against what the
+mathematics of a softmax at temperature T fixes (equal logits draw
+uniformly, a logit many T above the rest is always drawn, draw frequencies
+match exp(l/T)/sum over many seeded draws, scaling logits and T by the same
+power of two changes no draw), each check failed by a planted mistake.
 """
 
 import numpy as np
 
 
+def canonical(row):
+    """fp32 logits with -0.0 as +0.0 and every NaN's sign bit cleared."""
+    bits = np.asarray(row, dtype=np.float32).copy().view(np.uint32)
+    nan = (bits & np.uint32(0x7fffffff)) > np.uint32(0x7f800000)
+    bits[nan] &= np.uint32(0x7fffffff)
+    bits[bits == np.uint32(0x80000000)] = 0
+    return bits.view(np.float32)
+
+
 def candidates(row, k):
-    """(ids, logits) of the k largest fp32 logits of `row`, largest first,
-    equal logits by ascending id; rows shorter than k give all of them."""
-    ln = np.asarray(row, dtype=np.float32)
+    """(ids, logits) of the k largest fp32 logits of `row` in numpy's order
+    (NaN largest, -0 == +0), largest first, equal logits by ascending id;
+    rows shorter than k give all of them.  Logits come back canonical."""
+    ln = canonical(row)
     k = min(k, ln.shape[0])
-    # stable sort on -logit keeps ascending id among equal logits
-    order = np.argsort(-ln.astype(np.float64), kind="stable")[:k]
+    bits = ln.view(np.uint32).astype(np.int64)
+    # order-preserving integer of each canonical value (NaNs above +inf)
+    rank = np.where(bits >= 0x80000000, 0xffffffff - bits, bits + 0x80000000)
+    # stable sort on -rank keeps ascending id among equal logits
+    order = np.argsort(-rank, kind="stable")[:k]
     return order.astype(np.int64), ln[order]
 
 

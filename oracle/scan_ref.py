@@ -150,15 +150,6 @@ def contracted_scan_ref(delta, u, Bc, Cc, A_real, A_imag, track, n_state, checkp
     return torch.cat(outs, dim=1), (h, beta_last)
 
 
-def bidirectional_scan_ref(u, delta, A_real, A_imag, B, C, D, track, n_state):
-    """Bidirectional branch of Mamba3Block.forward (engine/mamba.py:254-260):
-    y = S(x) + flip(S(flip(x))), where S includes u * D (so the skip is 2uD)."""
-    y = selective_scan_ref(u, delta, A_real, A_imag, B, C, D, track, n_state)
-    y = y + selective_scan_ref(u.flip(1), delta.flip(1), A_real, A_imag,
-                               B.flip(1), C.flip(1), D, track, n_state).flip(1)
-    return y
-
-
 def step_core_ref(delta, u, Bc, Cc, A_real, A_imag, track, D, state):
     """SSM core of Mamba3Block.step (engine/mamba.py:466-494), fp32.
 

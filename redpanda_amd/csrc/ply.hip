@@ -27,10 +27,16 @@ namespace rp {
 
 namespace {
 
-// fp32 bits -> uint32 whose unsigned order is the IEEE total order of the
-// floats (-NaN < -inf < ... < -0 < +0 < ... < +inf < +NaN), and back.
+// fp32 bits -> uint32 whose unsigned order is numpy's order of the floats,
+// which the reference's argpartition / argsort apply: -inf < ... < +inf <
+// NaN, with -0 equal to +0 and every NaN above +inf whatever its sign.  The
+// key is that of the canonical value (+0 for -0, the NaN with its sign bit
+// cleared), so equal values tie and fall to the id order; key_value gives
+// the canonical value back.
 __device__ __forceinline__ uint32_t order_key(float v) {
-  const uint32_t b = __float_as_uint(v);
+  uint32_t b = __float_as_uint(v);
+  if ((b & 0x7fffffffu) > 0x7f800000u) b &= 0x7fffffffu;  // NaN of either sign
+  if (b == 0x80000000u) b = 0u;                           // -0
   return b ^ ((b & 0x80000000u) ? 0xffffffffu : 0x80000000u);
 }
 __device__ __forceinline__ float key_value(uint32_t k) {

@@ -38,7 +38,7 @@ def _check_topk(logits, k, values=None):
         n = len(ids)
         got_ids = h[r, k + 1:].view(np.int32)
         assert np.array_equal(got_ids[:n], ids), (r, got_ids, ids)
-        assert np.array_equal(h[r, 1:1 + n], lns)
+        assert np.array_equal(h[r, 1:1 + n].view(np.uint32), lns.view(np.uint32))
         assert np.all(got_ids[n:] == -1) and np.all(np.isneginf(h[r, 1 + n:1 + k]))
         if values is not None:
             assert h[r, 0] == values.cpu().numpy()[r]
@@ -66,20 +66,43 @@ def test_topk_ties_by_ascending_id(gpu_lib):
 
 
 def test_topk_special_values(gpu_lib):
-    x = torch.randn(4, 300)
+    x = torch.randn(5, 300)
     x[0, 17] = float("inf")
     x[1, 5] = float("-inf")
     x[2, :] = float("-inf")
     x[3, 100] = float("nan")
     x[3, 200] = float("inf")
+    x[4, :] = -1.0
+    x[4, 7] = -0.0
+    x[4, 3] = 0.0
+    x[4, 250] = -float("nan")
     from redpanda_amd.rollout import ply_topk
     out = ply_topk(x.to(dev), 4).cpu().numpy()
     ids = out[:, 5:].view(np.int32)
     assert ids[0, 0] == 17 and np.isposinf(out[0, 1])
     assert 5 not in ids[1]
     assert list(ids[2]) == [0, 1, 2, 3] and np.all(np.isneginf(out[2, 1:5]))
-    # IEEE total order: a positive NaN ranks above +inf
+    # numpy's order, as the reference's argpartition applies it: a NaN
+    # ranks above +inf, whatever its sign; -0 ties with +0 (ascending id)
     assert ids[3, 0] == 100 and np.isnan(out[3, 1]) and ids[3, 1] == 200
+    assert list(ids[4]) == [250, 3, 7, 0] and np.isnan(out[4, 1])
+    assert out[4, 3].view(np.uint32) == 0  # -0 comes back as +0
+
+
+def test_topk_tie_heavy_long_rows(gpu_lib):
+    """Integer-valued rows of 8192 with +-0 and NaNs of both signs: past the
+    first 1024-element block, where the wave-wide bound and the one-compare
+    filter decide which elements reach the lists."""
+    x = _rows(24, 8192, torch.float32, 9, ties=True).clone()
+    g = torch.Generator().manual_seed(10)
+    zero = torch.rand(x.shape, generator=g) < 0.05
+    x[zero.to(dev)] = -0.0
+    x[3, 5000] = float("nan")
+    x[4, 6000] = -float("nan")
+    x[5, 7000] = float("nan")
+    x[5, 100] = -float("nan")
+    _check_topk(x, 16)
+    _check_topk(x, 3)
 
 
 def test_gather_matches_oracle(gpu_lib):

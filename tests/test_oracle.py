@@ -336,27 +336,107 @@ def test_rollout_candidates_match_reference_expression():
         assert np.array_equal(lns, row[ids])
 
 
+def _numpy_order(row, k):
+    """Brute force of numpy's order on a tiny row: NaN (either sign) above
+    +inf, -0 equal to +0, equal values by ascending id."""
+    import math
+    key = lambda i: (0 if math.isnan(row[i]) else 1, 0.0 if math.isnan(row[i]) else -float(row[i]), i)
+    return sorted(range(len(row)), key=key)[:min(k, len(row))]
+
+
 def test_rollout_candidates_brute_force_and_ties():
-    """Brute force on tiny rows: the list is the k largest, descending, equal
-    logits by ascending id; nothing outside beats anything inside.  A planted
-    wrong order (ascending) fails the same check."""
-    import itertools
+    """Brute force on tiny rows with many ties, +-0, +-inf and NaNs of both
+    signs: the list is the k largest in numpy's order, equal logits by
+    ascending id; nothing outside beats anything inside.  A planted wrong
+    order (ascending) fails the same check."""
     import numpy as np
     from oracle import rollout_ref
     rng = np.random.default_rng(1)
-    for _ in range(200):
+    special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan], dtype=np.float32)
+    neg_nan = np.array([0xffc00000], dtype=np.uint32).view(np.float32)[0]
+    for _ in range(400):
         V = int(rng.integers(1, 9))
         k = int(rng.integers(1, 6))
-        row = rng.integers(-2, 3, V).astype(np.float32)  # many ties
+        row = rng.integers(-2, 3, V).astype(np.float32)
+        for i in range(V):
+            if rng.random() < 0.3:
+                row[i] = special[rng.integers(0, 5)] if rng.random() < 0.8 else neg_nan
         ids, lns = rollout_ref.candidates(row, k)
-        pairs = sorted(((-float(row[i]), i) for i in range(V)))[:min(k, V)]
-        assert [p[1] for p in pairs] == list(ids)
+        assert _numpy_order(row, k) == list(ids)
+        assert np.array_equal(lns.view(np.uint32), rollout_ref.canonical(row)[ids].view(np.uint32))
         rest = set(range(V)) - set(ids.tolist())
-        assert all(row[j] <= lns.min() for j in rest)
+        ranks = {i: r for r, i in enumerate(_numpy_order(row, V))}
+        assert all(ranks[j] > max(ranks[i] for i in ids) for j in rest)
         # a planted mistake (the k smallest, ascending) fails the same check
-        wrong = sorted(((float(row[i]), i) for i in range(V)))[:min(k, V)]
-        if len(set(row.tolist())) > 1:
-            assert [p[1] for p in wrong] != list(ids)
+        wrong = list(reversed(_numpy_order(row, V)))[:min(k, V)]
+        if len({(float(x) if x == x else "nan") for x in row}) > 1:
+            assert wrong != list(ids)
+
+
+def test_rollout_candidates_nan_against_reference_expr():
+    """One NaN in an otherwise tie-free row: the reference's own expression
+    (numpy's argpartition / argsort) puts it first, as candidates does."""
+    import numpy as np
+    from oracle import rollout_ref
+    rng = np.random.default_rng(2)
+    for V, k in [(300, 8), (40, 16), (9, 4)]:
+        for sign in (1, -1):
+            row = rng.standard_normal(V).astype(np.float32)
+            j = int(rng.integers(0, V))
+            row[j] = np.float32(np.nan) * sign
+            ids, _ = rollout_ref.candidates(row, k)
+            assert ids[0] == j
+            assert np.array_equal(ids, rollout_ref.candidates_reference_expr(row, k))
+
+
+def _draw_counts(select, logits, temp, n, seed):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    row = np.asarray(logits, dtype=np.float32)
+    counts = np.zeros(len(row), dtype=np.int64)
+    for _ in range(n):
+        counts[select(row, len(row), lambda t: True, temp, rng)] += 1
+    return counts
+
+
+def _softmax_ok(select, logits, temp, n=20000, seed=11):
+    """Draw frequencies within 4.5 sigma of exp(l / T) / sum (computed here
+    with math.exp, not the oracle's code)."""
+    import math
+    z = [math.exp(l / temp) for l in logits]
+    p = [x / sum(z) for x in z]
+    c = _draw_counts(select, logits, temp, n, seed)
+    return all(abs(c[i] - n * p[i]) <= 4.5 * math.sqrt(n * p[i] * (1 - p[i])) + 1e-9
+               for i in range(len(p)))
+
+
+def test_rollout_select_draw_is_the_softmax():
+    """The sampling branch of the walk (engine/mars_search.py:271-276),
+    pinned by what the mathematics fixes: equal logits draw uniformly, a logit
+    far above the rest is always drawn, frequencies match exp(l/T)/sum, and
+    scaling logits and T by the same power of two changes no draw.  Planted
+    mistakes (l*T for l/T, T ignored) fail."""
+    import numpy as np
+    from oracle import rollout_ref
+    sel = rollout_ref.select_move
+    assert _softmax_ok(sel, [1.0, 1.0, 1.0, 1.0], 0.7)
+    assert _softmax_ok(sel, [2.0, 1.0, 0.5, -1.0], 0.8)
+    assert _softmax_ok(sel, [0.3, -0.2, 0.1], 2.5)
+    dominant = _draw_counts(sel, [10.0, 0.0, 0.0, 0.0], 0.1, 2000, 3)
+    assert dominant[0] == 2000
+    a = [sel(np.array([2.0, 1.0, 0.5, -1.0], np.float32), 4, lambda t: True, 0.8,
+             np.random.default_rng(s)) for s in range(300)]
+    b = [sel(np.array([8.0, 4.0, 2.0, -4.0], np.float32), 4, lambda t: True, 3.2,
+             np.random.default_rng(s)) for s in range(300)]
+    assert a == b
+
+    def planted_product(row, k, is_legal, temp, rng):
+        return sel(np.asarray(row) * temp * temp, k, is_legal, temp, rng)  # l*T
+
+    def planted_no_temp(row, k, is_legal, temp, rng):
+        return sel(row, k, is_legal, 1.0, rng)
+    assert not _softmax_ok(planted_product, [2.0, 1.0, 0.5, -1.0], 0.8)
+    assert not _softmax_ok(planted_no_temp, [2.0, 1.0, 0.5, -1.0], 0.3)
 
 
 def test_rollout_gather_and_select_walk():
