@@ -42,6 +42,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "redpanda_hip.h"
 #include "rp_launch.h"
 #include "rp_sincos_table.h"
@@ -79,6 +81,22 @@ __device__ __forceinline__ float cvt_raw(uint32_t v, int dtype) {
 // Streamed-input load with on-the-fly conversion to fp32 (uniform dtype).
 __device__ __forceinline__ float load_in(const void* p, int64_t i, int dtype) {
   return cvt_raw(load_raw(p, i, dtype), dtype);
+}
+
+// The raw element type of storage code IT, as load_raw returns it widened.
+template <int IT>
+using RawOf = typename std::conditional<IT == RP_F32, uint32_t, uint16_t>::type;
+
+// Element i of a row given by a wave-uniform pointer, i a 32-bit lane offset:
+// the address form of a global access with a scalar base and a 32-bit vector
+// offset, so the lane's part costs no 64-bit arithmetic.
+template <class T>
+__device__ __forceinline__ T load_at(const void* row, uint32_t i) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(row) + i * (uint32_t)sizeof(T));
+}
+template <class T>
+__device__ __forceinline__ void store_at(void* row, uint32_t i, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(row) + i * (uint32_t)sizeof(T)) = v;
 }
 
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }

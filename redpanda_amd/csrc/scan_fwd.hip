@@ -19,12 +19,27 @@
 
 namespace rp {
 
+// Steps staged per block: fewer for large states, whose B / C rows dominate
+// the LDS (occupancy).
+template <int S, int NPL>
+constexpr int fwd_tb() { return S * NPL > 40 ? kFwdTB / 2 : kFwdTB; }
+
+// Workgroups per CU that the kernel's LDS allows (160 KB per CU), at most 7:
+// the register budget the compiler is held to, so that VGPRs do not limit
+// the occupancy below what the LDS gives (7 leaves the recurrence of every
+// shape its registers).
+template <int S, int NPL>
+constexpr int fwd_occupancy() {
+  constexpr int TB = fwd_tb<S, NPL>(), CB = kWaves * (kWave / S), NP = S * NPL;
+  constexpr int lds = TB * CB * 12 + 2 * TB * NP * 4 + kTab * 8;
+  return 163840 / lds < 7 ? 163840 / lds : 7;
+}
+
 template <int S, int NPL, class GK>
-__global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut o) {
+__global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_kernel(ScanParams p,
+                                                                                          FwdOut o) {
   using Sh = Shape<S, NPL>;
-  // steps staged per block: fewer for large states, whose B / C rows
-  // dominate the LDS (occupancy)
-  constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = NP > 40 ? kFwdTB / 2 : kFwdTB;
+  constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, TB = fwd_tb<S, NPL>();
   __shared__ float2 sDH[TB][CB];   // (dt, (dt*u)/2) per step and channel
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
@@ -46,6 +61,39 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
   fill_cos_lin(sCos, tid);  // first read after the staging barrier below
 
   const int nblk = (L + TB - 1) / TB;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // wave index, scalar
+  // Full blocks (all TB steps, every channel of the tile present) whose four
+  // streamed inputs share one storage type take the fast staging: rows are
+  // wave-uniform, so an address is a scalar row base plus the lane's fixed
+  // 32-bit offset, and each part issues all its loads before converting any.
+  // Channel rows: a wave instruction covers RW rows of CW channels (lane =
+  // rh * CW + ci0), NHC instructions per row, QC passes per wave.
+  constexpr int CW = CB < kWave ? CB : kWave, RW = kWave / CW, NHC = CB / CW;
+  constexpr int QC = TB / (kWaves * RW);
+  static_assert(QC * kWaves * RW == TB, "a block is whole passes of channel rows");
+  // State rows: one row per wave instruction, lane = LDS column kk (NH
+  // instructions per row), QB rows per wave.
+  constexpr int NH = (NP + kWave - 1) / kWave, QB = TB / kWaves;
+  static_assert(QB * kWaves == TB, "a block is whole passes of state rows");
+  const bool tile_full = (tile + 1) * CB <= p.D;
+  const bool one_type = p.dt_delta == p.dt_u && p.dt_u == p.dt_B && p.dt_B == p.dt_C;
+  constexpr int64_t kOffMax = 1ll << 29;  // lane offsets stay 32-bit byte offsets
+  const bool offs_fit = (int64_t)RW * (p.dsl + p.usl + p.D) + CB < kOffMax && p.N < kOffMax;
+  // The lane's place in the fast paths' row layouts, recomputed from an opaque
+  // copy of the lane index at every use: otherwise the compiler keeps the
+  // derived per-lane addresses live through the recurrence (registers).
+  auto lane_fresh = [&]() {
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    return l;
+  };
+  // Likewise the batch row and tile as scalars: the 64-bit row bases derived
+  // from them are recomputed per block instead of held in scalar registers.
+  auto row_tile_fresh = [&](int& bo, int& to) {
+    bo = b;
+    to = tile;
+    asm volatile("" : "+s"(bo), "+s"(to));
+  };
   for (int dir = 0; dir < p.ndir; ++dir) {
     // sm = h + hb of the previous step (of the initial state h0, beta0 / 2)
     float sm[NPL];
@@ -58,9 +106,56 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
         sm[j] = p.h0[idx] + 0.5f * p.beta0[idx];
       }
     }
+    // the lane's channel-row slot (rh, ci0), its row within a pass in time
+    // order, and its offsets into delta, u and the (B, L, D) arrays (y, the
+    // delta cache)
+    struct ChanLane {
+      int rh, ci0;
+      uint32_t od, ou, oy;
+    };
+    auto chan_lane = [&]() {
+      const int l = lane_fresh();
+      ChanLane cl;
+      cl.rh = l / CW;
+      cl.ci0 = l % CW;
+      const int rl = dir ? RW - 1 - cl.rh : cl.rh;
+      cl.od = rl * (uint32_t)p.dsl + cl.ci0;
+      cl.ou = rl * (uint32_t)p.usl + cl.ci0;
+      cl.oy = rl * (uint32_t)p.D + cl.ci0;
+      return cl;
+    };
+    // earliest time of the RW channel rows from block row rb
+    auto pass_t = [&](int i0, int rb) { return dir ? L - i0 - rb - RW : i0 + rb; };
     // y of the block starting at step i0 (cnt steps) from sY: coalesced, and
     // the reverse direction adds to what the forward direction stored
     auto write_y = [&](int i0, int cnt) {
+      if (cnt == TB && tile_full && offs_fit) {
+        const ChanLane ln = chan_lane();
+        const int rh = ln.rh, ci0 = ln.ci0;
+        const uint32_t oy = ln.oy;
+        int bo, to;
+        row_tile_fresh(bo, to);
+        float prev[QC][NHC];
+        if (dir == 1) {
+#pragma unroll
+          for (int q = 0; q < QC; ++q)
+#pragma unroll
+            for (int h = 0; h < NHC; ++h)
+              prev[q][h] = load_at<float>(
+                  o.y + ((int64_t)bo * L + pass_t(i0, (wv + kWaves * q) * RW)) * p.D + to * CB + h * CW, oy);
+        }
+#pragma unroll
+        for (int q = 0; q < QC; ++q) {
+          const int rb = (wv + kWaves * q) * RW;
+#pragma unroll
+          for (int h = 0; h < NHC; ++h) {
+            const float v = sY[rb + rh][h * CW + ci0];
+            store_at(o.y + ((int64_t)bo * L + pass_t(i0, rb)) * p.D + to * CB + h * CW, oy,
+                     dir == 0 ? v : prev[q][h] + v);
+          }
+        }
+        return;
+      }
       for (int e = tid; e < cnt * CB; e += kThreads) {
         const int r = e / CB, ci = e % CB;
         const int c2 = tile * CB + ci;
@@ -72,46 +167,146 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
         }
       }
     };
+    // fast staging of a full block, IT the common storage code (delta used
+    // as given: no softplus, no cache).  Row bases advance by a signed stride
+    // per pass (passes are kWaves * RW channel rows or kWaves state rows
+    // apart in the block).
+    auto stage_fast = [&](auto it_tag, int i0) {
+      constexpr int IT = decltype(it_tag)::value;
+      using Raw = RawOf<IT>;
+      const ChanLane ln = chan_lane();
+      const int rh = ln.rh, ci0 = ln.ci0;
+      const uint32_t od = ln.od, ou = ln.ou;
+      int bo, to;
+      row_tile_fresh(bo, to);
+      const int dtq = dir ? -kWaves * RW : kWaves * RW;  // time step between passes
+      const int64_t tq0 = pass_t(i0, wv * RW);
+      const Raw* drow = static_cast<const Raw*>(p.delta) + (int64_t)bo * p.dsb + tq0 * p.dsl + to * CB;
+      const Raw* urow = static_cast<const Raw*>(p.u) + (int64_t)bo * p.usb + tq0 * p.usl + to * CB;
+      const int64_t dstep = dtq * p.dsl, ustep = dtq * p.usl;
+      __builtin_amdgcn_sched_barrier(0);
+      Raw rd[QC][NHC], ru[QC][NHC];
+#pragma unroll
+      for (int q = 0; q < QC; ++q) {
+#pragma unroll
+        for (int h = 0; h < NHC; ++h) {
+          rd[q][h] = load_at<Raw>(drow + h * CW, od);
+          ru[q][h] = load_at<Raw>(urow + h * CW, ou);
+        }
+        drow += dstep;
+        urow += ustep;
+      }
+#pragma unroll
+      for (int q = 0; q < QC; ++q) {
+        const int rb = (wv + kWaves * q) * RW;
+#pragma unroll
+        for (int h = 0; h < NHC; ++h) {
+          const float dt = cvt_raw(rd[q][h], IT);
+          sDH[rb + rh][h * CW + ci0] = make_float2(dt, 0.5f * fmul(dt, cvt_raw(ru[q][h], IT)));
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // the state of each of the lane's LDS columns, clamped into the row for
+      // the load; columns past NP and pad states stage zeros
+      const int l = lane_fresh();
+      uint32_t nld[NH];
+      bool nval[NH];
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        const int kk = l + h * kWave;
+        const int n = kk < NP ? (kk % NPL) * S + kk / NPL : 0;
+        nld[h] = (uint32_t)min(n, p.N - 1);
+        nval[h] = kk < NP && n < p.N;
+      }
+      const int dts = dir ? -kWaves : kWaves;  // time step between state rows of a wave
+      const int64_t ts0 = dir ? L - 1 - i0 - wv : i0 + wv;
+      const Raw* brow = static_cast<const Raw*>(p.Bc) + (int64_t)bo * p.bsb + ts0 * p.bsl;
+      const Raw* cbrow = static_cast<const Raw*>(p.Cc) + (int64_t)bo * p.csb + ts0 * p.csl;
+      const int64_t bstep = dts * p.bsl, cbstep = dts * p.csl;
+      // in groups of QG state rows: at most 2 * QG * NH loads in flight, so
+      // the staging stays within the register budget of the recurrence
+      constexpr int QG = QB < 4 ? QB : 4;
+      static_assert(QB % QG == 0, "whole groups of state rows");
+#pragma unroll
+      for (int q0 = 0; q0 < QB; q0 += QG) {
+        __builtin_amdgcn_sched_barrier(0);
+        Raw rbv[QG][NH], rcv[QG][NH];
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+#pragma unroll
+          for (int h = 0; h < NH; ++h) {
+            rbv[q][h] = load_at<Raw>(brow, nld[h]);
+            rcv[q][h] = load_at<Raw>(cbrow, nld[h]);
+          }
+          brow += bstep;
+          cbrow += cbstep;
+        }
+#pragma unroll
+        for (int q = 0; q < QG; ++q) {
+          const int r = wv + kWaves * (q0 + q);
+#pragma unroll
+          for (int h = 0; h < NH; ++h) {
+            const int kk = l + h * kWave;
+            if (NH * kWave == NP || kk < NP) {
+              sB[r][kk] = nval[h] ? cvt_raw(rbv[q][h], IT) : 0.f;
+              sC[r][kk] = nval[h] ? cvt_raw(rcv[q][h], IT) : 0.f;
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
     for (int bi = 0; bi < nblk; ++bi) {
       const int i0 = bi * TB;
       const int cnt = min(TB, L - i0);
       __syncthreads();
       if (bi > 0) write_y(i0 - TB, TB);
-      for (int e = tid; e < TB * CB; e += kThreads) {
-        const int r = e / CB, ci = e % CB;
-        const int c2 = tile * CB + ci;
-        float dt = 0.f, hd = 0.f;
-        if (r < cnt && c2 < p.D) {
-          const int i = i0 + r;
-          const int t = dir ? (L - 1 - i) : i;
-          const int64_t di = ((int64_t)b * L + t) * p.D + c2;
-          if (dir == 1 && o.dcache != nullptr) {
-            dt = o.dcache[di];  // cached by this workgroup's forward direction
-          } else {
-            dt = load_in(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
-            if (p.dsp) dt = softplus_of(dt);
-            if (o.dcache != nullptr) o.dcache[di] = dt;
+      if (cnt == TB && tile_full && one_type && offs_fit && !p.dsp && o.dcache == nullptr) {
+        if (p.dt_B == RP_BF16)
+          stage_fast(std::integral_constant<int, RP_BF16>{}, i0);
+        else if (p.dt_B == RP_F32)
+          stage_fast(std::integral_constant<int, RP_F32>{}, i0);
+        else
+          stage_fast(std::integral_constant<int, RP_F16>{}, i0);
+      } else {
+        for (int e = tid; e < TB * CB; e += kThreads) {
+          const int r = e / CB, ci = e % CB;
+          const int c2 = tile * CB + ci;
+          float dt = 0.f, hd = 0.f;
+          if (r < cnt && c2 < p.D) {
+            const int i = i0 + r;
+            const int t = dir ? (L - 1 - i) : i;
+            const int64_t di = ((int64_t)b * L + t) * p.D + c2;
+            if (dir == 1 && o.dcache != nullptr) {
+              dt = o.dcache[di];  // cached by this workgroup's forward direction
+            } else {
+              dt = load_in(p.delta, (int64_t)b * p.dsb + (int64_t)t * p.dsl + c2, p.dt_delta);
+              if (p.dsp) dt = softplus_of(dt);
+              if (o.dcache != nullptr) o.dcache[di] = dt;
+            }
+            const float uu = load_in(p.u, (int64_t)b * p.usb + (int64_t)t * p.usl + c2, p.dt_u);
+            hd = 0.5f * fmul(dt, uu);
           }
-          const float uu = load_in(p.u, (int64_t)b * p.usb + (int64_t)t * p.usl + c2, p.dt_u);
-          hd = 0.5f * fmul(dt, uu);
+          sDH[r][ci] = make_float2(dt, hd);
         }
-        sDH[r][ci] = make_float2(dt, hd);
-      }
-      for (int e = tid; e < TB * NP; e += kThreads) {
-        const int r = e / NP, k = e % NP;
-        const int n = (k % NPL) * S + (k / NPL);
-        float bv = 0.f, cv = 0.f;
-        if (r < cnt && n < p.N) {
-          const int i = i0 + r;
-          const int t = dir ? (L - 1 - i) : i;
-          bv = load_in(p.Bc, (int64_t)b * p.bsb + (int64_t)t * p.bsl + n, p.dt_B);
-          cv = load_in(p.Cc, (int64_t)b * p.csb + (int64_t)t * p.csl + n, p.dt_C);
+        for (int e = tid; e < TB * NP; e += kThreads) {
+          const int r = e / NP, k = e % NP;
+          const int n = (k % NPL) * S + (k / NPL);
+          float bv = 0.f, cv = 0.f;
+          if (r < cnt && n < p.N) {
+            const int i = i0 + r;
+            const int t = dir ? (L - 1 - i) : i;
+            bv = load_in(p.Bc, (int64_t)b * p.bsb + (int64_t)t * p.bsl + n, p.dt_B);
+            cv = load_in(p.Cc, (int64_t)b * p.csb + (int64_t)t * p.csl + n, p.dt_C);
+          }
+          sB[r][k] = bv;
+          sC[r][k] = cv;
         }
-        sB[r][k] = bv;
-        sC[r][k] = cv;
       }
       __syncthreads();
-      for (int r = 0; r < cnt; ++r) {
+      // one step of the block (row r); i0 is a multiple of kCkptK, so the
+      // checkpoint steps are the rows r with (r + 1) % kCkptK == 0
+      auto step = [&](int r) {
         const int i = i0 + r;
         const float2 dh = sDH[r][cl];
         float h[NPL], hb[NPL];
@@ -119,7 +314,7 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
                                                  &sC[r][s * NPL], s, p.NR, has_imag);
         // the channel's S lanes hold the same total and store the same value
         sY[r][cl] = reduce_states<S>(y);
-        if (o.ckpt != nullptr && ((i + 1) % kCkptK) == 0 && i + 1 < L) {
+        if (o.ckpt != nullptr && ((r + 1) % kCkptK) == 0 && i + 1 < L) {
           // state entering chunk (i+1)/K, in a coalesced [tile][wave][j][lane] record
           const int64_t rec =
               ((int64_t)(dir * p.B + b) * p.nck + ((i + 1) / kCkptK - 1)) * p.ntiles + tile;
@@ -139,6 +334,17 @@ __global__ __launch_bounds__(kThreads) void scan_fwd_kernel(ScanParams p, FwdOut
             }
           }
         }
+      };
+      static_assert(TB % kCkptK == 0, "blocks start on checkpoint boundaries");
+      if (cnt == TB) {
+        // a full block in groups of kCkptK steps: LDS offsets and the
+        // checkpoint test are compile-time within a group
+        for (int r0 = 0; r0 < TB; r0 += kCkptK) {
+#pragma unroll
+          for (int k = 0; k < kCkptK; ++k) step(r0 + k);
+        }
+      } else {
+        for (int r = 0; r < cnt; ++r) step(r);
       }
     }
     if (nblk > 0) {

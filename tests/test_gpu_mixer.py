@@ -51,8 +51,8 @@ def _inputs(B, L, D, dt=torch.float32, seed=0, z_view=True):
 def _close(a, b, rtol, what, scale=None):
     """|a - b| <= rtol * (|b| + scale) element-wise (scale: the magnitude of
     the terms that cancel in b, where they do)."""
-    a, b = a.float(), b.float()
-    ref = b.abs() if scale is None else b.abs() + scale.float()
+    a, b = a.detach().float(), b.detach().float()
+    ref = b.abs() if scale is None else b.abs() + scale.detach().float()
     err = ((a - b).abs() / (ref + 1e-30)).where(ref != 0, (a - b).abs())
     assert float(err.max()) <= rtol, f"{what}: max rel err {float(err.max()):.3e} > {rtol:.1e}"
 
