@@ -65,7 +65,18 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   constexpr bool ALT = NPL <= 3 || (NPL == 4 && S >= 8) ||
                        (NPL == 5 && S == 8 && GK::kRJ == NPL - 1 && GK::kTJ == NPL - 1);
   constexpr int DT = Sh::kDT, CB = Sh::kCB, NP = Sh::kNP, K = kCkptK;
-  constexpr int KR = NP <= 40 ? K : K / 2;  // steps per channel-sum fold
+  // Steps per channel-sum fold: one fold (two barriers) per chunk up to 40
+  // states and for 16 lanes x 5 slots with the last slot tracking in every
+  // lane (N 65-80 with 64 rotational states, the long-sequence shape:
+  // measured 1.7 % faster), two folds elsewhere above 40 states (a whole
+  // chunk's row partials spilled registers there and measured 3-5 % slower).
+  // Above 40 states a whole chunk's row partials take the LDS that the
+  // per-thread float64 parameter sums would: those then go to their global
+  // per-batch-group partials instead (the same additions in the same order).
+  constexpr bool FOLD_CHUNK = S * NPL <= 40 || (S == 16 && NPL == 5 && GK::kImag == 1 &&
+                                                GK::kRJ == NPL - 1 && GK::kTJ == NPL - 1);
+  constexpr int KR = FOLD_CHUNK ? K : K / 2;
+  constexpr bool PAR_GLOBAL = S * NPL > 40 && FOLD_CHUNK;
   constexpr int NFOLD = K / KR;             // folds per chunk
   constexpr int NRW = kWaves * 4;           // 16-lane rows per workgroup
   // row partials of one output are contiguous (4 x 16-byte reads); the
@@ -88,8 +99,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
   __shared__ float2 sCS[kTab];              // (m, b sin) records of the gate table
   // per-thread float64 sums of the parameter gradients over the batch group
-  // (dA_real or dtrack, dA_imag), kept in LDS to spare registers
-  __shared__ double sPar[2][NPL][kThreads];
+  // (dA_real or dtrack, dA_imag), kept in LDS to spare registers (in their
+  // global partials when PAR_GLOBAL)
+  __shared__ double sPar[PAR_GLOBAL ? 1 : 2][PAR_GLOBAL ? 1 : NPL][PAR_GLOBAL ? 1 : kThreads];
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
@@ -108,11 +120,21 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // pam: the coefficient of the ddt sum over rotational states, zero for a
   // tracking state (only read for slots whose kind is decided at run time)
   float pam[NPL];
+  // this thread's entry for state slot j of the per-batch-group partials
+  // (dA_real or dtrack; dA_imag is one D*N block further)
+  auto par_at = [&](int j) { return ((int64_t)bgi * 2) * p.D * p.N + (int64_t)c * p.N + j * S + s; };
 #pragma unroll
   for (int j = 0; j < NPL; ++j) {
     pam[j] = is_rot<S, GK>(j, s, p.NR) ? gp.pah[j] : 0.f;
-    sPar[0][j][tid] = 0.0;
-    sPar[1][j][tid] = 0.0;
+    if constexpr (PAR_GLOBAL) {
+      if (cvalid && j * S + s < p.N) {
+        io.part_par[par_at(j)] = 0.0;
+        io.part_par[par_at(j) + (int64_t)p.D * p.N] = 0.0;
+      }
+    } else {
+      sPar[0][j][tid] = 0.0;
+      sPar[1][j][tid] = 0.0;
+    }
   }
 
   // time index of forward-order step i in this direction
@@ -467,8 +489,15 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
             for (int j = 0; j < NPL; ++j) {
               const float a = (j >= GK::kRJ && j < GK::kTJ && !is_rot<S, GK>(j, s, p.NR)) ? cpt[j]
                                                                                           : cpa[j];
-              sPar[0][j][tid] += (double)a;
-              if (j < GK::kTJ) sPar[1][j][tid] += (double)cpb[j];
+              if constexpr (PAR_GLOBAL) {
+                if (cvalid && j * S + s < p.N) {
+                  io.part_par[par_at(j)] += (double)a;
+                  if (j < GK::kTJ) io.part_par[par_at(j) + (int64_t)p.D * p.N] += (double)cpb[j];
+                }
+              } else {
+                sPar[0][j][tid] += (double)a;
+                if (j < GK::kTJ) sPar[1][j][tid] += (double)cpb[j];
+              }
               cpa[j] = 0.f;
               cpb[j] = 0.f;
               cpt[j] = 0.f;
@@ -503,14 +532,16 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     }
   }
   // per-batch-group parameter-gradient partials (float64)
-  if (cvalid) {
+  if constexpr (!PAR_GLOBAL) {
+    if (cvalid) {
 #pragma unroll
-    for (int j = 0; j < NPL; ++j) {
-      const int n = j * S + s;
-      if (n < p.N) {
-        const int64_t base = ((int64_t)bgi * 2) * p.D * p.N;
-        io.part_par[base + (int64_t)c * p.N + n] = sPar[0][j][tid];
-        io.part_par[base + (int64_t)p.D * p.N + (int64_t)c * p.N + n] = sPar[1][j][tid];
+      for (int j = 0; j < NPL; ++j) {
+        const int n = j * S + s;
+        if (n < p.N) {
+          const int64_t base = ((int64_t)bgi * 2) * p.D * p.N;
+          io.part_par[base + (int64_t)c * p.N + n] = sPar[0][j][tid];
+          io.part_par[base + (int64_t)p.D * p.N + (int64_t)c * p.N + n] = sPar[1][j][tid];
+        }
       }
     }
   }
