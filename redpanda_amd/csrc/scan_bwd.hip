@@ -490,9 +490,16 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               const float a = (j >= GK::kRJ && j < GK::kTJ && !is_rot<S, GK>(j, s, p.NR)) ? cpt[j]
                                                                                           : cpa[j];
               if constexpr (PAR_GLOBAL) {
+                // float64 atomic adds whose result is not used: nothing waits
+                // on a load.  Only this thread updates these entries, and its
+                // accesses to one address execute in program order, so the
+                // sums are the same, in the same order, as a load-add-store
+                // (bitwise-identical results; the reduction kernel reads them
+                // after this kernel ends).
                 if (cvalid && j * S + s < p.N) {
-                  io.part_par[par_at(j)] += (double)a;
-                  if (j < GK::kTJ) io.part_par[par_at(j) + (int64_t)p.D * p.N] += (double)cpb[j];
+                  unsafeAtomicAdd(&io.part_par[par_at(j)], (double)a);
+                  if (j < GK::kTJ)
+                    unsafeAtomicAdd(&io.part_par[par_at(j) + (int64_t)p.D * p.N], (double)cpb[j]);
                 }
               } else {
                 sPar[0][j][tid] += (double)a;
