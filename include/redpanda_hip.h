@@ -100,8 +100,9 @@ typedef struct rp_scan_fwd_out {
  * (B, D, N) fp32 gradients of the final state returned by a causal forward
  * (training through prime_cache + step, engine/search_mamba.py:252-273).
  * d_h0, d_beta0: NULL, or (B, D, N) fp32 outputs receiving the gradient of
- * the initial state h0 / beta0 (requires h0).  Deterministic: no float
- * atomics.
+ * the initial state h0 / beta0 (requires h0).  Deterministic: every sum
+ * runs in a fixed order (the float atomic adds some shapes use each update
+ * an address that no other thread touches).
  */
 typedef struct rp_scan_bwd_io {
   const float* dy;

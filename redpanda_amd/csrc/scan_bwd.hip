@@ -32,14 +32,16 @@
 // direction) are likewise loaded a chunk ahead.  The chunk code is
 // instantiated per slot, so every LDS address is a compile-time offset.
 //
-// Reductions, all in a fixed order (run-to-run deterministic, no atomics):
+// Reductions, all in a fixed order (run-to-run deterministic; no address is
+// updated by more than one thread):
 //   * over a channel's states (ddt, du): in-lane FMA chain + DPP butterfly;
 //   * over channels (dB, dC): DPP row rotations inside each 16-lane row, the
 //     row partials staged in LDS, then a balanced 16-way sum per output, per tile;
 //     the per-tile partials are summed in float64 by a second kernel;
 //   * parameter gradients (dA, dTk): fp32 sums over up to 16 chunks (64
-//     steps) accumulated in float64 per lane over the batch group, then
-//     float64 across groups.
+//     steps) accumulated in float64 per lane over the batch group (above 40
+//     states per channel, in the group's global partials by atomic adds that
+//     only that lane makes), then float64 across groups.
 
 #include <type_traits>
 
