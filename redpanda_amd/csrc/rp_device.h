@@ -98,6 +98,20 @@ template <class T>
 __device__ __forceinline__ void store_at(void* row, uint32_t i, T v) {
   *reinterpret_cast<T*>(static_cast<char*>(row) + i * (uint32_t)sizeof(T)) = v;
 }
+// The same with the lane's part given in bytes.
+template <class T>
+__device__ __forceinline__ T load_byte(const void* base, uint32_t off) {
+  return *reinterpret_cast<const T*>(static_cast<const char*>(base) + off);
+}
+template <class T>
+__device__ __forceinline__ void store_byte(void* base, uint32_t off, T v) {
+  *reinterpret_cast<T*>(static_cast<char*>(base) + off) = v;
+}
+// A streamed-input element as stored (load_raw's result) at a byte offset.
+__device__ __forceinline__ uint32_t load_raw_byte(const void* base, uint32_t off, int dtype) {
+  if (dtype == RP_F32) return load_byte<uint32_t>(base, off);
+  return load_byte<uint16_t>(base, off);
+}
 
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }
 

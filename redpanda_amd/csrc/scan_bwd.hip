@@ -54,7 +54,15 @@ namespace rp {
 // added into the float64 sums (64 steps).
 constexpr int kParChunks = 16;
 
-template <int S, int NPL, class GK>
+// FAST: the instantiation for launches with no initial state, no final-state
+// gradients and every channel of every tile present, whose arrays span less
+// than 4 GiB each (bwd_fast below).  Every global address of the chunk loop
+// is then a wave-uniform base pointer plus a 32-bit byte offset, taken per
+// batch-row sweep and moved by a uniform multiple of the chunk index: one
+// full-rate add per staged element, where the general form multiplies 64-bit
+// indices per element and chunk.  Both instantiations compute the same
+// values in the same order.
+template <int S, int NPL, class GK, bool FAST>
 __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
   using Sh = Shape<S, NPL>;
   // ALT: the entry state is prefetched into two buffers that alternate with
@@ -112,7 +120,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   const int wrow = wave * 4 + lane / 16;  // row index within the workgroup
   const int tile = blockIdx.x % p.ntiles, bgi = blockIdx.x / p.ntiles;
   const int c = tile * CB + cl;
-  const bool cvalid = c < p.D;
+  const bool cvalid = FAST || c < p.D;
   const bool has_imag = p.Ai != nullptr;
   const int L = p.L;
 
@@ -153,7 +161,106 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   const int64_t d_sb = cached ? (int64_t)L * p.D : p.dsb;
   const int64_t d_sl = cached ? (int64_t)p.D : p.dsl;
   const int d_dt = cached ? RP_F32 : p.dt_delta;
+  // FAST: this thread's byte offsets for the sweep (b, dir) as they would be
+  // at chunk 0, and the wave-uniform byte step per chunk: the offset at chunk
+  // ch is o + ch * step (mod 2^32; the elements a lane loads or stores lie in
+  // their arrays, whose spans fit in 32 bits).  oF is relative to the
+  // sweep's (tile, b) block of the dB / dC partials, pbc.
+  uint32_t oDT[CPT], oU[CPT], oDY[CPT], oB[SPT], oC[SPT], oF[NFOLD][FPT], oD[DPT];
+  uint32_t stDT = 0, stU = 0, stDY = 0, stB = 0, stC = 0, stF = 0;
+  float* pbc = io.part_bc;
+  // FAST: fold output k of this thread as LDS float index * 8 + its row
+  // within the fold, or -1 beyond the fold's outputs
+  int fInfo[FPT];
+  if constexpr (FAST) {
+#pragma unroll
+    for (int k = 0; k < FPT; ++k) {
+      const int e = tid + k * kThreads;
+      fInfo[k] = -1;
+      if (e < KR * 2 * p.N) {
+        const int rr = e / (2 * p.N), rem = e % (2 * p.N);
+        const int which = rem / p.N, n = rem % p.N;
+        const int kk = (n % S) * NPL + n / S;
+        fInfo[k] = (((rr * 2 + which) * NP + kk) * RWP) * 8 + rr;
+      }
+    }
+  }
+  auto fast_sweep = [&](int b, int dir) {
+    const int64_t sg = dir ? -1 : 1;  // time steps per forward-order step
+    const int64_t t0 = dir ? L - 1 : 0;
+    const int64_t es_d = d_dt == RP_F32 ? 4 : 2, es_u = p.dt_u == RP_F32 ? 4 : 2;
+    const int64_t es_b = p.dt_B == RP_F32 ? 4 : 2, es_c = p.dt_C == RP_F32 ? 4 : 2;
+#pragma unroll
+    for (int k = 0; k < CPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int64_t t = t0 + sg * (e / CB - 1), c2 = tile * CB + e % CB;
+      oDT[k] = (uint32_t)((b * d_sb + t * d_sl + c2) * es_d);
+      oU[k] = (uint32_t)((b * p.usb + t * p.usl + c2) * es_u);
+      oDY[k] = (uint32_t)((((int64_t)b * L + t) * p.D + c2) * 4);
+    }
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int kk = e % NP;
+      const int64_t t = t0 + sg * (e / NP - 1), n = (kk % NPL) * S + kk / NPL;
+      oB[k] = (uint32_t)((b * p.bsb + t * p.bsl + n) * es_b);
+      oC[k] = (uint32_t)((b * p.csb + t * p.csl + n) * es_c);
+    }
+    const int64_t half = (int64_t)p.ntiles * p.B * L * p.N;  // the dC half of the partials
+#pragma unroll
+    for (int f = 0; f < NFOLD; ++f) {
+#pragma unroll
+      for (int k = 0; k < FPT; ++k) {
+        const int e = tid + k * kThreads;
+        const int rr = e / (2 * p.N), rem = e % (2 * p.N);
+        const int64_t t = t0 + sg * (f * KR + rr);
+        oF[f][k] = (uint32_t)(((rem / p.N) * half + t * p.N + rem % p.N) * 4);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int e = tid + k * kThreads;
+      const int64_t t = t0 + sg * (e / CB), c2 = tile * CB + e % CB;
+      oD[k] = (uint32_t)((((int64_t)b * L + t) * p.D + c2) * 4);
+    }
+    stDT = (uint32_t)(sg * K * d_sl * es_d);
+    stU = (uint32_t)(sg * K * p.usl * es_u);
+    stDY = (uint32_t)(sg * K * p.D * 4);
+    stB = (uint32_t)(sg * K * p.bsl * es_b);
+    stC = (uint32_t)(sg * K * p.csl * es_c);
+    stF = (uint32_t)(sg * K * p.N * 4);
+    pbc = io.part_bc + ((int64_t)tile * p.B + b) * L * p.N;
+  };
   auto stage_load = [&](int b, int dir, int ch) {
+    if constexpr (FAST) {
+      const uint32_t cu = (uint32_t)ch;
+#pragma unroll
+      for (int k = 0; k < CPT; ++k) {
+        const int e = tid + k * kThreads;
+        const int i = ch * K + e / CB - 1;
+        rdt[k] = 0u;
+        ru[k] = 0u;
+        rdy[k] = 0.f;
+        if (e < KS * CB && (unsigned)i < (unsigned)L) {
+          rdt[k] = load_raw_byte(dsrc, oDT[k] + cu * stDT, d_dt);
+          ru[k] = load_raw_byte(p.u, oU[k] + cu * stU, p.dt_u);
+          rdy[k] = load_byte<float>(io.dy, oDY[k] + cu * stDY);
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < SPT; ++k) {
+        const int e = tid + k * kThreads;
+        const int kk = e % NP;
+        const int i = ch * K + e / NP - 1;
+        rb[k] = 0u;
+        rc[k] = 0u;
+        if (e < KS * NP && (kk % NPL) * S + kk / NPL < p.N && (unsigned)i < (unsigned)L) {
+          rb[k] = load_raw_byte(p.Bc, oB[k] + cu * stB, p.dt_B);
+          rc[k] = load_raw_byte(p.Cc, oC[k] + cu * stC, p.dt_C);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int e = tid + k * kThreads;
@@ -209,6 +316,20 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // h entering chunk `chunk` of this lane's states: the forward's checkpoint,
   // or for chunk 0 the initial state (zero unless h0 is given, causal only)
   auto load_entry_h = [&](int chunk, int b, int dir, float (&dst)[NPL]) {
+    if constexpr (FAST) {
+      // no initial state: zero entering chunk 0
+      if (chunk == 0) {
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) dst[j] = 0.f;
+      } else {
+        const int64_t rec = ((int64_t)(dir * p.B + b) * p.nck + (chunk - 1)) * p.ntiles + tile;
+        const float* src =
+            io.ckpt + (rec * kWaves + __builtin_amdgcn_readfirstlane(wave)) * (NPL * kWave);
+#pragma unroll
+        for (int j = 0; j < NPL; ++j) dst[j] = load_at<float>(src, (uint32_t)(lane + j * kWave));
+      }
+      return;
+    }
     if (chunk == 0) {
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
@@ -255,13 +376,16 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       // gq: the g_{t+1} q_{t+1} term of q_t;  gr: the term of dhb_t.  They are
       // equal except at the last step, where an outside consumer of the final
       // state contributes dh_last to q and 2*dbeta_last to dhb.
+      // (FAST has no final-state gradients: gr equals gq throughout and is
+      // not kept.)
       float gq[NPL], gr[NPL];
+      if constexpr (FAST) fast_sweep(b, dir);
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
         const int n = j * S + s;
         gq[j] = 0.f;
         gr[j] = 0.f;
-        if (dir == 0 && cvalid && n < p.N) {
+        if (!FAST && dir == 0 && cvalid && n < p.N) {
           const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
           if (io.dh_last != nullptr) gq[j] = io.dh_last[idx];
           if (io.dbeta_last != nullptr) gr[j] = 2.f * io.dbeta_last[idx];
@@ -311,7 +435,10 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 #pragma unroll
             for (int k = 0; k < FPT; ++k) {
               prev[f][k] = 0.f;
-              if (dir == 1) {
+              if constexpr (FAST) {
+                if (dir == 1 && fInfo[k] >= 0 && f * KR + (fInfo[k] & 7) < kcnt)
+                  prev[f][k] = load_byte<float>(pbc, oF[f][k] + (uint32_t)ch * stF);
+              } else if (dir == 1) {
                 const float* src = fold_dst(tid + k * kThreads, b, dir, i0, f * KR, kcnt);
                 if (src != nullptr) prev[f][k] = *src;
               }
@@ -321,7 +448,14 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           for (int k = 0; k < DPT; ++k) {
             pdd[k][0] = 0.f;
             pdd[k][1] = 0.f;
-            if (dir == 1) {
+            if constexpr (FAST) {
+              const int e = tid + k * kThreads;
+              if (dir == 1 && e < K * CB && e / CB < kcnt) {
+                const uint32_t o = oD[k] + (uint32_t)ch * stDY;
+                pdd[k][0] = load_byte<float>(io.d_delta, o);
+                pdd[k][1] = load_byte<float>(io.d_u, o);
+              }
+            } else if (dir == 1) {
               const int64_t idx = dd_index(tid + k * kThreads, b, dir, i0, kcnt);
               if (idx >= 0) {
                 pdd[k][0] = io.d_delta[idx];
@@ -358,7 +492,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
             for (int j = 0; j < NPL; ++j) {
               const int n = j * S + s;
               hbp[j] = 0.f;
-              if (dir == 0 && p.h0 != nullptr && cvalid && n < p.N)
+              if (!FAST && dir == 0 && p.h0 != nullptr && cvalid && n < p.N)
                 hbp[j] = 0.5f * p.beta0[((int64_t)b * p.D + c) * p.N + n];
             }
           } else {
@@ -412,7 +546,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 else
                   ht = ffma(g, SP[m][j], fmul(hd, Bv));
                 const float q = ffma(dy, Cv, gq[j]);
-                const float dhb = q + gr[j];
+                const float dhb = q + (FAST ? gq[j] : gr[j]);
                 sBc = ffma(dhb, Bv, sBc);
                 const float dg = fmul(q, SP[m][j]);
                 if (j >= GK::kTJ) {  // tracking in every lane
@@ -429,7 +563,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   ddB = ffma(gp.wh[j], t2, ddB);                          // Ai 256/(2 pi) dg e sin
                 }
                 gq[j] = fmul(g, q);
-                gr[j] = gq[j];
+                if constexpr (!FAST) gr[j] = gq[j];
                 // every lane of the row holds the row's total for its slice
                 // s, so the lanes sharing s store the same value
                 sRed[m % KR][0][s * NPL + j][wrow] = reduce_row<S>(fmul(dhb, hd));
@@ -452,6 +586,18 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               __syncthreads();
 #pragma unroll
               for (int k = 0; k < FPT; ++k) {
+                if constexpr (FAST) {
+                  if (fInfo[k] >= 0 && (FULL || m + (fInfo[k] & 7) < kcnt)) {
+                    const float4* rp =
+                        reinterpret_cast<const float4*>(&sRed[0][0][0][0] + (fInfo[k] >> 3));
+                    const float4 a0 = rp[0], a1 = rp[1], a2 = rp[2], a3 = rp[3];
+                    const float v = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
+                                    (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
+                    store_byte<float>(pbc, oF[m / KR][k] + (uint32_t)ch * stF,
+                                      dir == 0 ? v : prev[m / KR][k] + v);
+                  }
+                  continue;
+                }
                 const int e = tid + k * kThreads;
                 float* dst = fold_dst(e, b, dir, i0, m, kcnt);
                 if (dst != nullptr) {
@@ -470,6 +616,18 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 #pragma unroll
                 for (int k = 0; k < DPT; ++k) {
                   const int e = tid + k * kThreads;
+                  if constexpr (FAST) {
+                    if (e < K * CB && (FULL || e / CB < kcnt)) {
+                      const uint32_t o = oD[k] + (uint32_t)ch * stDY;
+                      const float2 v = sDD[e / CB][e % CB];
+                      float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
+                      if (p.dsp && dd_final(dir))
+                        dd = softplus_grad_from_delta(dd, sCh[SL][e / CB + 1][e % CB].x);
+                      store_byte<float>(io.d_delta, o, dd);
+                      store_byte<float>(io.d_u, o, dir == 0 ? v.y : pdd[k][1] + v.y);
+                    }
+                    continue;
+                  }
                   const int64_t idx = dd_index(e, b, dir, i0, kcnt);
                   if (idx >= 0) {
                     const float2 v = sDD[e / CB][e % CB];
@@ -527,7 +685,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       }
       // after the sweep gq = g_0 q_0: the gradient of the initial state, since
       // h_0 = g_0 (h0 + beta0/2) + hb_0
-      if (dir == 0 && io.d_h0 != nullptr && cvalid) {
+      if (!FAST && dir == 0 && io.d_h0 != nullptr && cvalid) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           const int n = j * S + s;
@@ -594,10 +752,35 @@ __global__ void bwd_reduce_par(const double* __restrict__ part, float* __restric
   }
 }
 
+// Whether a launch takes the FAST instantiation: no initial state and no
+// final-state gradients, every tile's channels present, and every array the
+// chunk loop addresses spanning less than 4 GiB (its byte offsets then fit
+// in 32 bits).
+static bool bwd_fast(const ScanParams& p, const BwdIO& io, int CB) {
+  if (p.h0 != nullptr || io.dh_last != nullptr || io.dbeta_last != nullptr || io.d_h0 != nullptr)
+    return false;
+  if (p.D % CB != 0) return false;
+  const int64_t lim = (int64_t)1 << 32;
+  auto es = [](int dt) { return (int64_t)(dt == RP_F32 ? 4 : 2); };
+  // one past the last byte of a (B, L, inner) array with strides sb, sl
+  auto span = [&](int64_t sb, int64_t sl, int64_t inner, int64_t e) {
+    return ((p.B - 1) * sb + (p.L - 1) * sl + inner) * e;
+  };
+  const bool cached = p.dsp != 0;
+  const int64_t dspan = cached ? (int64_t)p.B * p.L * p.D * 4 : span(p.dsb, p.dsl, p.D, es(p.dt_delta));
+  const int64_t half = (int64_t)p.ntiles * p.B * p.L * p.N;
+  return dspan < lim && span(p.usb, p.usl, p.D, es(p.dt_u)) < lim &&
+         span(p.bsb, p.bsl, p.N, es(p.dt_B)) < lim && span(p.csb, p.csl, p.N, es(p.dt_C)) < lim &&
+         (int64_t)p.B * p.L * p.D * 4 < lim && (half + (int64_t)p.L * p.N) * 4 < lim;
+}
+
 template <int S, int NPL, class GK>
 static hipError_t launch_bwd_t(const ScanParams& p, const BwdIO& io, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ntiles * io.nbg));
-  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK>), grid, dim3(kThreads), 0, st, p, io);
+  if (bwd_fast(p, io, Shape<S, NPL>::kCB))
+    hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, true>), grid, dim3(kThreads), 0, st, p, io);
+  else
+    hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, false>), grid, dim3(kThreads), 0, st, p, io);
   return hipGetLastError();
 }
 
