@@ -465,11 +465,21 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           }
           if (ch > 0) load_entry_h(ch - 1, b, dir, next);
         };
+        // The entry state into hc, waited for here: its loads were issued a
+        // chunk earlier and have completed.  The opaque use keeps the wait
+        // before this chunk's own loads; at a later first use it would also
+        // wait for those (loads complete in issue order).
+        auto take_entry = [&](const float (&src)[NPL]) {
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) {
+            hc[j] = src[j];
+            asm volatile("" : "+v"(hc[j]));
+          }
+        };
         if constexpr (!ALT) {
           // the entry state is copied out of the one prefetch buffer, which
           // then receives the next chunk's
-#pragma unroll
-          for (int j = 0; j < NPL; ++j) hc[j] = hE[0][j];
+          take_entry(hE[0]);
           issue_loads(hE[0]);
         }
         // The chunk body, instantiated for FULL (all K steps present, the
@@ -480,8 +490,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           constexpr int SL = decltype(slot_tag)::value;
           if constexpr (ALT) {
             // the entry state, taken before this chunk issues its loads
-#pragma unroll
-            for (int j = 0; j < NPL; ++j) hc[j] = hE[SL][j];
+            take_entry(hE[SL]);
             issue_loads(hE[1 - SL]);
           }
           // hb entering the chunk: from the step before (row 0 of the slot;
