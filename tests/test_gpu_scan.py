@@ -256,6 +256,29 @@ def test_backward_is_deterministic(gpu_lib):
             assert torch.equal(g1[k], g2[k]), k
 
 
+@pytest.mark.parametrize("NR,NT,D", [(12, 4, 128), (32, 8, 64), (64, 8, 48)])
+@pytest.mark.parametrize("softplus", [False, True])
+def test_whole_tile_backward_equals_general(gpu_lib, NR, NT, D, softplus):
+    """The backward's whole-tile instantiation (no initial state, no final-state
+    gradients, D a multiple of the tile) against its general one on the same
+    causal scan, taken by passing an all-zero initial state and all-zero
+    final-state gradients: every output bit for bit (L=37 ends in a partial
+    chunk)."""
+    c = make_case(505, B=3, L=37, D=D, NR=NR, NT=NT)
+    if softplus:
+        c["delta"] = torch.randn(c["delta"].shape, generator=torch.Generator().manual_seed(5)) - 2
+    N = NR + NT
+    y1, g1 = hip_capi.scan_fwd_bwd(c, softplus=softplus)
+    zero = torch.zeros(3, D, N)
+    y2, g2 = hip_capi.scan_fwd_bwd(c, dh_last=zero, dbeta_last=zero, softplus=softplus)
+    y3, g3 = hip_capi.scan_fwd_bwd(c, h0=zero, beta0=zero, softplus=softplus)
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)
+    for k in g1:
+        if g1[k] is not None:
+            assert torch.equal(g1[k], g2[k]), f"final-state gradients, {k}"
+            assert torch.equal(g1[k], g3[k]), f"initial state, {k}"
+
+
 def test_linearity_in_u(gpu_lib):
     scan, _ = _scan()
     c = make_case(501, B=2, L=40, D=64, NR=12, NT=4)

@@ -36,7 +36,7 @@ def _backward(entry, c, bidirectional):
     rp_scan_bwd (a workspace) or not at all (rp_scan_bwd_noalloc)."""
     lib = _lib.load()
     _, ckpt, _, (a, keep) = hip_capi.scan_fwd(c, bidirectional, with_ckpt=True)
-    _, u, Bc, Cc, Ar, Ai, Tk = keep
+    _, u, Bc, Cc, Ar, Ai, Tk = keep[:7]
     B, L, D = u.shape
     N = Bc.shape[-1]
     f32 = dict(dtype=torch.float32, device="cuda")
