@@ -35,7 +35,13 @@ constexpr int fwd_occupancy() {
   return 163840 / lds < 7 ? 163840 / lds : 7;
 }
 
-template <int S, int NPL, class GK>
+// MODEL: the instantiation for the model's launches, whose full blocks take
+// the fast staging with delta as the dt projection x (the scan uses
+// softplus(x), kept in the delta cache by the first direction and read back
+// by the second), delta and u in bf16 or fp16 (autocast) and B, C in fp32
+// (the fused BCNorm's output).  A separate instantiation: the other kernel's
+// fast staging keeps its registers.
+template <int S, int NPL, class GK, bool MODEL>
 __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_kernel(ScanParams p,
                                                                                           FwdOut o) {
   using Sh = Shape<S, NPL>;
@@ -167,42 +173,77 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
         }
       }
     };
-    // fast staging of a full block, IT the common storage code (delta used
-    // as given: no softplus, no cache).  Row bases advance by a signed stride
-    // per pass (passes are kWaves * RW channel rows or kWaves state rows
-    // apart in the block).
-    auto stage_fast = [&](auto it_tag, int i0) {
-      constexpr int IT = decltype(it_tag)::value;
-      using Raw = RawOf<IT>;
+    // fast staging of a full block: ITC the storage code of delta and u, ITS
+    // that of B and C; DSP: delta holds x and the scan uses softplus(x),
+    // cached in o.dcache (when given) by the first direction and read back
+    // by the second (the generic staging's order of operations).  Row bases
+    // advance by a signed stride per pass (passes are kWaves * RW channel
+    // rows or kWaves state rows apart in the block).
+    auto stage_fast = [&](auto itc_tag, auto its_tag, auto dsp_tag, int i0) {
+      constexpr int ITC = decltype(itc_tag)::value, ITS = decltype(its_tag)::value;
+      constexpr bool DSP = decltype(dsp_tag)::value;
+      using Raw = RawOf<ITC>;
+      using RawS = RawOf<ITS>;
       const ChanLane ln = chan_lane();
       const int rh = ln.rh, ci0 = ln.ci0;
-      const uint32_t od = ln.od, ou = ln.ou;
+      const uint32_t od = ln.od, ou = ln.ou, oy = ln.oy;
       int bo, to;
       row_tile_fresh(bo, to);
       const int dtq = dir ? -kWaves * RW : kWaves * RW;  // time step between passes
       const int64_t tq0 = pass_t(i0, wv * RW);
       const Raw* drow = static_cast<const Raw*>(p.delta) + (int64_t)bo * p.dsb + tq0 * p.dsl + to * CB;
       const Raw* urow = static_cast<const Raw*>(p.u) + (int64_t)bo * p.usb + tq0 * p.usl + to * CB;
-      const int64_t dstep = dtq * p.dsl, ustep = dtq * p.usl;
+      // the delta cache's rows (y's layout); with DSP, the second direction
+      // reads softplus(x) from it
+      float* crow = DSP && o.dcache != nullptr ? o.dcache + ((int64_t)bo * L + tq0) * p.D + to * CB
+                                               : nullptr;
+      const bool from_cache = DSP && dir == 1 && crow != nullptr;
+      const int64_t dstep = dtq * p.dsl, ustep = dtq * p.usl, cstep = (int64_t)dtq * p.D;
       __builtin_amdgcn_sched_barrier(0);
-      Raw rd[QC][NHC], ru[QC][NHC];
+      // delta as stored, or (DSP) the cached fp32 bits
+      typename std::conditional<DSP, uint32_t, Raw>::type rd[QC][NHC];
+      Raw ru[QC][NHC];
+      if (from_cache) {
+        const float* cr = crow;
 #pragma unroll
-      for (int q = 0; q < QC; ++q) {
+        for (int q = 0; q < QC; ++q) {
 #pragma unroll
-        for (int h = 0; h < NHC; ++h) {
-          rd[q][h] = load_at<Raw>(drow + h * CW, od);
-          ru[q][h] = load_at<Raw>(urow + h * CW, ou);
+          for (int h = 0; h < NHC; ++h) {
+            rd[q][h] = load_at<uint32_t>(cr + h * CW, oy);
+            ru[q][h] = load_at<Raw>(urow + h * CW, ou);
+          }
+          cr += cstep;
+          urow += ustep;
         }
-        drow += dstep;
-        urow += ustep;
+      } else {
+#pragma unroll
+        for (int q = 0; q < QC; ++q) {
+#pragma unroll
+          for (int h = 0; h < NHC; ++h) {
+            rd[q][h] = load_at<Raw>(drow + h * CW, od);
+            ru[q][h] = load_at<Raw>(urow + h * CW, ou);
+          }
+          drow += dstep;
+          urow += ustep;
+        }
       }
 #pragma unroll
       for (int q = 0; q < QC; ++q) {
         const int rb = (wv + kWaves * q) * RW;
 #pragma unroll
         for (int h = 0; h < NHC; ++h) {
-          const float dt = cvt_raw(rd[q][h], IT);
-          sDH[rb + rh][h * CW + ci0] = make_float2(dt, 0.5f * fmul(dt, cvt_raw(ru[q][h], IT)));
+          float dt;
+          if constexpr (DSP) {
+            if (from_cache) {
+              dt = __uint_as_float(rd[q][h]);
+            } else {
+              dt = softplus_of(cvt_raw(rd[q][h], ITC));
+              if (crow != nullptr) store_at(crow + q * cstep + h * CW, oy, dt);
+            }
+          } else {
+            dt = cvt_raw(rd[q][h], ITC);
+          }
+          sDH[rb + rh][h * CW + ci0] = make_float2(dt, 0.5f * fmul(dt, cvt_raw(ru[q][h], ITC)));
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -220,8 +261,8 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
       }
       const int dts = dir ? -kWaves : kWaves;  // time step between state rows of a wave
       const int64_t ts0 = dir ? L - 1 - i0 - wv : i0 + wv;
-      const Raw* brow = static_cast<const Raw*>(p.Bc) + (int64_t)bo * p.bsb + ts0 * p.bsl;
-      const Raw* cbrow = static_cast<const Raw*>(p.Cc) + (int64_t)bo * p.csb + ts0 * p.csl;
+      const RawS* brow = static_cast<const RawS*>(p.Bc) + (int64_t)bo * p.bsb + ts0 * p.bsl;
+      const RawS* cbrow = static_cast<const RawS*>(p.Cc) + (int64_t)bo * p.csb + ts0 * p.csl;
       const int64_t bstep = dts * p.bsl, cbstep = dts * p.csl;
       // in groups of QG state rows: at most 2 * QG * NH loads in flight, so
       // the staging stays within the register budget of the recurrence
@@ -230,13 +271,13 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
 #pragma unroll
       for (int q0 = 0; q0 < QB; q0 += QG) {
         __builtin_amdgcn_sched_barrier(0);
-        Raw rbv[QG][NH], rcv[QG][NH];
+        RawS rbv[QG][NH], rcv[QG][NH];
 #pragma unroll
         for (int q = 0; q < QG; ++q) {
 #pragma unroll
           for (int h = 0; h < NH; ++h) {
-            rbv[q][h] = load_at<Raw>(brow, nld[h]);
-            rcv[q][h] = load_at<Raw>(cbrow, nld[h]);
+            rbv[q][h] = load_at<RawS>(brow, nld[h]);
+            rcv[q][h] = load_at<RawS>(cbrow, nld[h]);
           }
           brow += bstep;
           cbrow += cbstep;
@@ -248,8 +289,8 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
           for (int h = 0; h < NH; ++h) {
             const int kk = l + h * kWave;
             if (NH * kWave == NP || kk < NP) {
-              sB[r][kk] = nval[h] ? cvt_raw(rbv[q][h], IT) : 0.f;
-              sC[r][kk] = nval[h] ? cvt_raw(rcv[q][h], IT) : 0.f;
+              sB[r][kk] = nval[h] ? cvt_raw(rbv[q][h], ITS) : 0.f;
+              sC[r][kk] = nval[h] ? cvt_raw(rcv[q][h], ITS) : 0.f;
             }
           }
         }
@@ -261,13 +302,23 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
       const int cnt = min(TB, L - i0);
       __syncthreads();
       if (bi > 0) write_y(i0 - TB, TB);
-      if (cnt == TB && tile_full && one_type && offs_fit && !p.dsp && o.dcache == nullptr) {
-        if (p.dt_B == RP_BF16)
-          stage_fast(std::integral_constant<int, RP_BF16>{}, i0);
-        else if (p.dt_B == RP_F32)
-          stage_fast(std::integral_constant<int, RP_F32>{}, i0);
+      using BF16 = std::integral_constant<int, RP_BF16>;
+      using F32 = std::integral_constant<int, RP_F32>;
+      using F16 = std::integral_constant<int, RP_F16>;
+      if (MODEL && cnt == TB && tile_full && offs_fit) {
+        // (the host launches MODEL only for its storage types, with softplus)
+        if (p.dt_u == RP_BF16)
+          stage_fast(BF16{}, F32{}, std::true_type{}, i0);
         else
-          stage_fast(std::integral_constant<int, RP_F16>{}, i0);
+          stage_fast(F16{}, F32{}, std::true_type{}, i0);
+      } else if (!MODEL && cnt == TB && tile_full && one_type && offs_fit && !p.dsp &&
+                 o.dcache == nullptr) {
+        if (p.dt_B == RP_BF16)
+          stage_fast(BF16{}, BF16{}, std::false_type{}, i0);
+        else if (p.dt_B == RP_F32)
+          stage_fast(F32{}, F32{}, std::false_type{}, i0);
+        else
+          stage_fast(F16{}, F16{}, std::false_type{}, i0);
       } else {
         for (int e = tid; e < TB * CB; e += kThreads) {
           const int r = e / CB, ci = e % CB;
@@ -357,7 +408,13 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
 template <int S, int NPL, class GK>
 static hipError_t launch_fwd_t(const ScanParams& p, const FwdOut& o, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ntiles * p.B));
-  hipLaunchKernelGGL((scan_fwd_kernel<S, NPL, GK>), grid, dim3(kThreads), 0, st, p, o);
+  // the model's launches: softplus, delta and u in bf16 or fp16, B and C in fp32
+  const bool model = p.dsp && p.dt_delta == p.dt_u && (p.dt_u == RP_BF16 || p.dt_u == RP_F16) &&
+                     p.dt_B == RP_F32 && p.dt_C == RP_F32;
+  if (model)
+    hipLaunchKernelGGL((scan_fwd_kernel<S, NPL, GK, true>), grid, dim3(kThreads), 0, st, p, o);
+  else
+    hipLaunchKernelGGL((scan_fwd_kernel<S, NPL, GK, false>), grid, dim3(kThreads), 0, st, p, o);
   return hipGetLastError();
 }
 
