@@ -593,6 +593,19 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               // fold the 16 row partials of steps [m, m + KR) into this
               // tile's global dB / dC partials
               __syncthreads();
+              // The reverse direction's prior values, waited for here (their
+              // loads were issued at the chunk's start).  Stores count with
+              // the loads in the same in-order counter, so a wait placed at a
+              // later first use would also wait for the stores issued before
+              // it, one memory round trip per store.
+              if (m == 0) {
+#pragma unroll
+                for (int f = 0; f < NFOLD; ++f)
+#pragma unroll
+                  for (int k = 0; k < FPT; ++k) asm volatile("" : "+v"(prev[f][k]));
+#pragma unroll
+                for (int k = 0; k < DPT; ++k) asm volatile("" : "+v"(pdd[k][0]), "+v"(pdd[k][1]));
+              }
 #pragma unroll
               for (int k = 0; k < FPT; ++k) {
                 if constexpr (FAST) {
