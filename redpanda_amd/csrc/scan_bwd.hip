@@ -418,6 +418,13 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
         else
           stage_store(Slot1{});
         __syncthreads();
+        // the first entry state waited for here too, so that on entering the
+        // chunk loop no load is pending into its registers (the loop's waits
+        // are placed for both ways in)
+#pragma unroll
+        for (int a = 0; a < (ALT ? 2 : 1); ++a)
+#pragma unroll
+          for (int j = 0; j < NPL; ++j) asm volatile("" : "+v"(hE[a][j]));
       }
 
       for (int ch = nct - 1; ch >= 0; --ch) {
@@ -598,6 +605,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               // the loads in the same in-order counter, so a wait placed at a
               // later first use would also wait for the stores issued before
               // it, one memory round trip per store.
+              // Likewise the next chunk's entry state: the loop's register
+              // copies at its back edge would otherwise wait for these stores.
               if (m == 0) {
 #pragma unroll
                 for (int f = 0; f < NFOLD; ++f)
@@ -605,6 +614,10 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   for (int k = 0; k < FPT; ++k) asm volatile("" : "+v"(prev[f][k]));
 #pragma unroll
                 for (int k = 0; k < DPT; ++k) asm volatile("" : "+v"(pdd[k][0]), "+v"(pdd[k][1]));
+#pragma unroll
+                for (int a = 0; a < (ALT ? 2 : 1); ++a)
+#pragma unroll
+                  for (int j = 0; j < NPL; ++j) asm volatile("" : "+v"(hE[a][j]));
               }
 #pragma unroll
               for (int k = 0; k < FPT; ++k) {
