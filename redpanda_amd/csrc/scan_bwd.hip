@@ -86,7 +86,16 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   constexpr bool FOLD_CHUNK = S * NPL <= 40 || (S == 16 && NPL == 5 && GK::kImag == 1 &&
                                                 GK::kRJ == NPL - 1 && GK::kTJ == NPL - 1);
   constexpr int KR = FOLD_CHUNK ? K : K / 2;
-  constexpr bool PAR_GLOBAL = S * NPL > 40 && FOLD_CHUNK;
+  // ONEBAR (FAST, one fold per chunk, up to 40 states): the row partials
+  // and the (d_delta, d_u) sit in one of two buffers by the chunk's slot, so
+  // no wave can overwrite a buffer before every wave has folded it (the next
+  // writer of a buffer is two chunks on, past the next chunk's barrier) and
+  // a chunk ends without the second barrier.  The second buffers take the
+  // LDS of the per-thread float64 parameter sums, which then go to their
+  // global partials (the same additions in the same order).
+  constexpr bool ONEBAR = FAST && FOLD_CHUNK && S * NPL <= 40;
+  constexpr int NB = ONEBAR ? 2 : 1;  // row-partial and (d_delta, d_u) buffers
+  constexpr bool PAR_GLOBAL = (S * NPL > 40 && FOLD_CHUNK) || ONEBAR;
   constexpr int NFOLD = K / KR;             // folds per chunk
   constexpr int NRW = kWaves * 4;           // 16-lane rows per workgroup
   // row partials of one output are contiguous (4 x 16-byte reads); the
@@ -105,8 +114,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float4 sCh[2][KS][CB];       // input slots: (dt, (dt*u)/2, u/2, dy)
   __shared__ float sB[2][KS][NP];
   __shared__ float sC[2][KS][NP];
-  __shared__ __align__(16) float sRed[KR][2][NP][RWP];  // per-row channel sums of dB, dC
-  __shared__ float2 sDD[K][CB];           // (d_delta, d_u) of the chunk
+  __shared__ __align__(16) float sRed[NB][KR][2][NP][RWP];  // per-row channel sums of dB, dC
+  __shared__ float2 sDD[NB][K][CB];       // (d_delta, d_u) of the chunk
   __shared__ float2 sCS[kTab];              // (m, b sin) records of the gate table
   // per-thread float64 sums of the parameter gradients over the batch group
   // (dA_real or dtrack, dA_imag), kept in LDS to spare registers (in their
@@ -582,8 +591,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 if constexpr (!FAST) gr[j] = gq[j];
                 // every lane of the row holds the row's total for its slice
                 // s, so the lanes sharing s store the same value
-                sRed[m % KR][0][s * NPL + j][wrow] = reduce_row<S>(fmul(dhb, hd));
-                sRed[m % KR][1][s * NPL + j][wrow] = reduce_row<S>(fmul(dy, ht));
+                sRed[ONEBAR ? SL : 0][m % KR][0][s * NPL + j][wrow] = reduce_row<S>(fmul(dhb, hd));
+                sRed[ONEBAR ? SL : 0][m % KR][1][s * NPL + j][wrow] = reduce_row<S>(fmul(dy, ht));
               }
               // d(gate)/d(dt) summed over the lane's states, then over the
               // channel's lanes with sBc; the channel's S lanes hold identical
@@ -592,9 +601,21 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               sBc = reduce_states<S>(sBc);
               const float ddt = dga + fmul(uh, sBc);
               const float dut = fmul(0.5f * dt, sBc);
-              sDD[m][cl] = make_float2(ddt, dut);
+              sDD[ONEBAR ? SL : 0][m][cl] = make_float2(ddt, dut);
             }
             if (m % KR == 0) {
+              // ONEBAR: with softplus, the factor -expm1(-delta) of each
+              // d_delta element, read while the slot is still this chunk's
+              // (without the second barrier another wave may restage it)
+              float fsp[DPT];
+              if (ONEBAR && m == 0 && p.dsp && dd_final(dir)) {
+#pragma unroll
+                for (int k = 0; k < DPT; ++k) {
+                  const int e = tid + k * kThreads;
+                  const int ee = e < K * CB ? e : 0;
+                  fsp[k] = -expm1f(-sCh[SL][ee / CB + 1][ee % CB].x);
+                }
+              }
               // the inputs of chunk ch-1 into the other slot
               if (m == 0 && ch >= 1) stage_store(std::integral_constant<int, 1 - SL>{});
               // fold the 16 row partials of steps [m, m + KR) into this
@@ -624,7 +645,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 if constexpr (FAST) {
                   if (fInfo[k] >= 0 && (FULL || m + (fInfo[k] & 7) < kcnt)) {
                     const float4* rp =
-                        reinterpret_cast<const float4*>(&sRed[0][0][0][0] + (fInfo[k] >> 3));
+                        reinterpret_cast<const float4*>(&sRed[ONEBAR ? SL : 0][0][0][0][0] + (fInfo[k] >> 3));
                     const float4 a0 = rp[0], a1 = rp[1], a2 = rp[2], a3 = rp[3];
                     const float v = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
                                     (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
@@ -639,7 +660,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   const int rem = e % (2 * p.N);
                   const int which = rem / p.N, n = rem % p.N;
                   const int kk = (n % S) * NPL + n / S;
-                  const float4* rp = reinterpret_cast<const float4*>(&sRed[e / (2 * p.N)][which][kk][0]);
+                  const float4* rp = reinterpret_cast<const float4*>(&sRed[0][e / (2 * p.N)][which][kk][0]);
                   const float4 a0 = rp[0], a1 = rp[1], a2 = rp[2], a3 = rp[3];
                   const float v = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
                                   (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
@@ -654,10 +675,11 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   if constexpr (FAST) {
                     if (e < K * CB && (FULL || e / CB < kcnt)) {
                       const uint32_t o = oD[k] + (uint32_t)ch * stDY;
-                      const float2 v = sDD[e / CB][e % CB];
+                      const float2 v = sDD[ONEBAR ? SL : 0][e / CB][e % CB];
                       float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
                       if (p.dsp && dd_final(dir))
-                        dd = softplus_grad_from_delta(dd, sCh[SL][e / CB + 1][e % CB].x);
+                        dd = ONEBAR ? fmul(dd, fsp[k])
+                                    : softplus_grad_from_delta(dd, sCh[SL][e / CB + 1][e % CB].x);
                       store_byte<float>(io.d_delta, o, dd);
                       store_byte<float>(io.d_u, o, dir == 0 ? v.y : pdd[k][1] + v.y);
                     }
@@ -665,7 +687,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   }
                   const int64_t idx = dd_index(e, b, dir, i0, kcnt);
                   if (idx >= 0) {
-                    const float2 v = sDD[e / CB][e % CB];
+                    const float2 v = sDD[0][e / CB][e % CB];
                     float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
                     // with softplus, the complete gradient is taken through it
                     // (delta of the element: row e / CB + 1 of the slot)
@@ -676,7 +698,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   }
                 }
               }
-              __syncthreads();
+              if constexpr (!ONEBAR) __syncthreads();
             }
           }
           if (ch % kParChunks == 0) {
