@@ -240,34 +240,78 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     stF = (uint32_t)(sg * K * p.N * 4);
     pbc = io.part_bc + ((int64_t)tile * p.B + b) * L * p.N;
   };
+  // FAST: the storage codes of (delta as staged, u, B and C) as one of the
+  // common combinations, fixed at compile time in the staging code, so that
+  // a staging branches once on them instead of once per element (-1: codes
+  // read at run time)
+  const int tcombo =
+      !FAST ? -1
+      : (d_dt == RP_BF16 && p.dt_u == RP_BF16 && p.dt_B == RP_BF16 && p.dt_C == RP_BF16) ? 0
+      : (d_dt == RP_F32 && p.dt_u == RP_F32 && p.dt_B == RP_F32 && p.dt_C == RP_F32)     ? 1
+      : (d_dt == RP_F32 && p.dt_u == RP_BF16 && p.dt_B == RP_F32 && p.dt_C == RP_F32)    ? 2
+      : (d_dt == RP_F32 && p.dt_u == RP_F16 && p.dt_B == RP_F32 && p.dt_C == RP_F32)     ? 3
+      : (d_dt == RP_F16 && p.dt_u == RP_F16 && p.dt_B == RP_F16 && p.dt_C == RP_F16)     ? 4
+                                                                                          : -1;
+  using TBF = std::integral_constant<int, RP_BF16>;
+  using TF32 = std::integral_constant<int, RP_F32>;
+  using TF16 = std::integral_constant<int, RP_F16>;
+  using TRT = std::integral_constant<int, -1>;
+  auto with_types = [&](auto f) {
+    switch (tcombo) {
+      case 0: f(TBF{}, TBF{}, TBF{}); break;
+      case 1: f(TF32{}, TF32{}, TF32{}); break;
+      case 2: f(TF32{}, TBF{}, TF32{}); break;
+      case 3: f(TF32{}, TF16{}, TF32{}); break;
+      case 4: f(TF16{}, TF16{}, TF16{}); break;
+      default: f(TRT{}, TRT{}, TRT{}); break;
+    }
+  };
+  // an element as stored (type IT, or the run-time code rt when IT is -1),
+  // and its value
+  auto load_t = [&](auto it_tag, const void* base, uint32_t off, int rt) -> uint32_t {
+    constexpr int IT = decltype(it_tag)::value;
+    if constexpr (IT < 0)
+      return load_raw_byte(base, off, rt);
+    else
+      return load_byte<RawOf<IT>>(base, off);
+  };
+  auto cvt_t = [&](auto it_tag, uint32_t v, int rt) -> float {
+    constexpr int IT = decltype(it_tag)::value;
+    if constexpr (IT < 0)
+      return cvt_raw(v, rt);
+    else
+      return cvt_raw(v, IT);
+  };
   auto stage_load = [&](int b, int dir, int ch) {
     if constexpr (FAST) {
       const uint32_t cu = (uint32_t)ch;
+      with_types([&](auto tdt, auto tu, auto ts) {
 #pragma unroll
-      for (int k = 0; k < CPT; ++k) {
-        const int e = tid + k * kThreads;
-        const int i = ch * K + e / CB - 1;
-        rdt[k] = 0u;
-        ru[k] = 0u;
-        rdy[k] = 0.f;
-        if (e < KS * CB && (unsigned)i < (unsigned)L) {
-          rdt[k] = load_raw_byte(dsrc, oDT[k] + cu * stDT, d_dt);
-          ru[k] = load_raw_byte(p.u, oU[k] + cu * stU, p.dt_u);
-          rdy[k] = load_byte<float>(io.dy, oDY[k] + cu * stDY);
+        for (int k = 0; k < CPT; ++k) {
+          const int e = tid + k * kThreads;
+          const int i = ch * K + e / CB - 1;
+          rdt[k] = 0u;
+          ru[k] = 0u;
+          rdy[k] = 0.f;
+          if (e < KS * CB && (unsigned)i < (unsigned)L) {
+            rdt[k] = load_t(tdt, dsrc, oDT[k] + cu * stDT, d_dt);
+            ru[k] = load_t(tu, p.u, oU[k] + cu * stU, p.dt_u);
+            rdy[k] = load_byte<float>(io.dy, oDY[k] + cu * stDY);
+          }
         }
-      }
 #pragma unroll
-      for (int k = 0; k < SPT; ++k) {
-        const int e = tid + k * kThreads;
-        const int kk = e % NP;
-        const int i = ch * K + e / NP - 1;
-        rb[k] = 0u;
-        rc[k] = 0u;
-        if (e < KS * NP && (kk % NPL) * S + kk / NPL < p.N && (unsigned)i < (unsigned)L) {
-          rb[k] = load_raw_byte(p.Bc, oB[k] + cu * stB, p.dt_B);
-          rc[k] = load_raw_byte(p.Cc, oC[k] + cu * stC, p.dt_C);
+        for (int k = 0; k < SPT; ++k) {
+          const int e = tid + k * kThreads;
+          const int kk = e % NP;
+          const int i = ch * K + e / NP - 1;
+          rb[k] = 0u;
+          rc[k] = 0u;
+          if (e < KS * NP && (kk % NPL) * S + kk / NPL < p.N && (unsigned)i < (unsigned)L) {
+            rb[k] = load_t(ts, p.Bc, oB[k] + cu * stB, p.dt_B);
+            rc[k] = load_t(ts, p.Cc, oC[k] + cu * stC, p.dt_C);
+          }
         }
-      }
+      });
       return;
     }
 #pragma unroll
@@ -302,6 +346,28 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   };
   auto stage_store = [&](auto slot_tag) {
     constexpr int SL = decltype(slot_tag)::value;
+    if constexpr (FAST) {
+      with_types([&](auto tdt, auto tu, auto ts) {
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+          const int e = tid + k * kThreads;
+          if (e < KS * CB) {
+            const float dt = cvt_t(tdt, rdt[k], d_dt);
+            const float uu = cvt_t(tu, ru[k], p.dt_u);
+            sCh[SL][e / CB][e % CB] = make_float4(dt, 0.5f * fmul(dt, uu), 0.5f * uu, rdy[k]);
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < SPT; ++k) {
+          const int e = tid + k * kThreads;
+          if (e < KS * NP) {
+            sB[SL][e / NP][e % NP] = cvt_t(ts, rb[k], p.dt_B);
+            sC[SL][e / NP][e % NP] = cvt_t(ts, rc[k], p.dt_C);
+          }
+        }
+      });
+      return;
+    }
 #pragma unroll
     for (int k = 0; k < CPT; ++k) {
       const int e = tid + k * kThreads;
