@@ -181,12 +181,19 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // FAST: fold output k of this thread as LDS float index * 8 + its row
   // within the fold, or -1 beyond the fold's outputs
   int fInfo[FPT];
+  // FAST: fold output of this thread in round k; the last, partial round
+  // runs on the last waves (the d_delta / d_u outputs run on the first)
+  constexpr int FREM = KR * 2 * NP - (FPT - 1) * kThreads;  // outputs in the last round
+  auto fold_e = [&](int k) {
+    if (k < FPT - 1) return tid + k * kThreads;
+    return tid < kThreads - FREM ? -1 : tid + k * kThreads - (kThreads - FREM);
+  };
   if constexpr (FAST) {
 #pragma unroll
     for (int k = 0; k < FPT; ++k) {
-      const int e = tid + k * kThreads;
+      const int e = fold_e(k);
       fInfo[k] = -1;
-      if (e < KR * 2 * p.N) {
+      if (e >= 0 && e < KR * 2 * p.N) {
         const int rr = e / (2 * p.N), rem = e % (2 * p.N);
         const int which = rem / p.N, n = rem % p.N;
         const int kk = (n % S) * NPL + n / S;
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     for (int f = 0; f < NFOLD; ++f) {
 #pragma unroll
       for (int k = 0; k < FPT; ++k) {
-        const int e = tid + k * kThreads;
+        const int e = fold_e(k);
         const int rr = e / (2 * p.N), rem = e % (2 * p.N);
         const int64_t t = t0 + sg * (f * KR + rr);
         oF[f][k] = (uint32_t)(((rem / p.N) * half + t * p.N + rem % p.N) * 4);

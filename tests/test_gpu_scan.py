@@ -256,14 +256,18 @@ def test_backward_is_deterministic(gpu_lib):
             assert torch.equal(g1[k], g2[k]), k
 
 
-@pytest.mark.parametrize("NR,NT,D", [(12, 4, 128), (32, 8, 64), (64, 8, 48)])
+@pytest.mark.parametrize("NR,NT,D", [(12, 4, 128), (16, 4, 128), (32, 8, 64), (24, 9, 64),
+                                     (40, 8, 48), (56, 8, 48), (64, 8, 48), (88, 8, 48),
+                                     (120, 8, 48)])
 @pytest.mark.parametrize("softplus", [False, True])
 def test_whole_tile_backward_equals_general(gpu_lib, NR, NT, D, softplus):
     """The backward's whole-tile instantiation (no initial state, no final-state
     gradients, D a multiple of the tile) against its general one on the same
     causal scan, taken by passing an all-zero initial state and all-zero
     final-state gradients: every output bit for bit (L=37 ends in a partial
-    chunk)."""
+    chunk).  The state counts cover every lane split (4, 8 and 16 lanes per
+    channel, 1 to 8 states per lane, padded slots) and so every way the
+    channel-sum fold's outputs divide into rounds over the workgroup."""
     c = make_case(505, B=3, L=37, D=D, NR=NR, NT=NT)
     if softplus:
         c["delta"] = torch.randn(c["delta"].shape, generator=torch.Generator().manual_seed(5)) - 2
