@@ -9,7 +9,29 @@ namespace rp {
 
 // dB / dC: sum the per-tile partials in a fixed order (fp64 accumulator).
 // The loads do not depend on the sum, so the unrolled loop keeps 8 of them in
-// flight while the additions stay in tile order.
+// flight while the additions stay in tile order.  bwd_reduce_bc4 sums four
+// adjacent elements per thread with 16-byte loads (the same additions in the
+// same order), for (B*L*N) a multiple of 4 and 16-byte aligned partials,
+// dB and dC.
+__global__ void bwd_reduce_bc4(const float4* __restrict__ part, float4* __restrict__ dB,
+                               float4* __restrict__ dC, int64_t per4, int ntiles) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= 2 * per4) return;
+  const int which = e >= per4;
+  const int64_t k = which ? e - per4 : e;
+  const float4* src = part + (int64_t)which * ntiles * per4 + k;
+  double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+#pragma unroll 8
+  for (int g = 0; g < ntiles; ++g) {
+    const float4 v = src[(int64_t)g * per4];
+    a0 += v.x;
+    a1 += v.y;
+    a2 += v.z;
+    a3 += v.w;
+  }
+  (which ? dC : dB)[k] = make_float4((float)a0, (float)a1, (float)a2, (float)a3);
+}
+
 __global__ void bwd_reduce_bc(const float* __restrict__ part, float* __restrict__ dB,
                               float* __restrict__ dC, int64_t per, int ntiles) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -90,7 +112,14 @@ hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const Bw
 hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
                                float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st) {
   const int64_t per = (int64_t)p.B * p.L * p.N;
-  if (per > 0) {
+  auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+  if (per > 0 && per % 4 == 0 && al16(io.part_bc) && al16(d_Bc) && al16(d_Cc)) {
+    const int64_t n = 2 * (per / 4);
+    hipLaunchKernelGGL(bwd_reduce_bc4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       (const float4*)io.part_bc, (float4*)d_Bc, (float4*)d_Cc, per / 4, p.ntiles);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  } else if (per > 0) {
     const int64_t n = 2 * per;
     hipLaunchKernelGGL(bwd_reduce_bc, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                        (const float*)io.part_bc, d_Bc, d_Cc, per, p.ntiles);

@@ -34,7 +34,8 @@
 //
 // Reductions, all in a fixed order (run-to-run deterministic; no address is
 // updated by more than one thread):
-//   * over a channel's states (ddt, du): in-lane FMA chain + DPP butterfly;
+//   * over a channel's states (ddt, du): in-lane FMA chain, then the S lanes'
+//     partials summed pairwise from LDS where the chunk's outputs are written;
 //   * over channels (dB, dC): DPP row rotations inside each 16-lane row, the
 //     row partials staged in LDS, then a balanced 16-way sum per output, per tile;
 //     the per-tile partials are summed in float64 by a second kernel;
@@ -117,7 +118,13 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   __shared__ float sB[2][KS][NP];
   __shared__ float sC[2][KS][NP];
   __shared__ __align__(16) float sRed[NB][KR][2][NP][RWP];  // per-row channel sums of dB, dC
-  __shared__ float2 sDD[NB][K][CB];       // (d_delta, d_u) of the chunk
+  // per lane: its (d gate / d dt, dhb . B) sums over its states of each
+  // chunk step, summed over the channel's S lanes where the chunk's
+  // (d_delta, d_u) are written.  Channel-contiguous per lane slice s; the
+  // row of a slice padded to CB + 16/S so that 16 lanes' writes (16/S
+  // channels x S slices) meet 32 distinct banks.
+  constexpr int DDP = CB + 16 / S;
+  __shared__ float2 sDD[NB][K][S][DDP];
   __shared__ float2 sCS[kTab];              // (m, b sin) records of the gate table
   // per-thread float64 sums of the parameter gradients over the batch group
   // (dA_real or dtrack, dA_imag), kept in LDS to spare registers (in their
@@ -447,6 +454,20 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     if (e >= K * CB || r >= kcnt || c2 >= p.D) return -1;
     return ((int64_t)b * L + tix(dir, i0 + r)) * p.D + c2;
   };
+  // (d_delta, d_u) of one chunk step and channel from its S lanes' partial
+  // sums (d gate / d dt, dhb . B) in sDD: the sums over the lanes in the
+  // order of reduce_states (pairwise, adjacent halves), then
+  //     d_delta = dga + (dt*u)/2 * sBc,   d_u = dt/2 * sBc
+  auto dd_of = [&](int buf, int r, int cc, float dt, float uh) -> float2 {
+    float2 v[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) v[i] = sDD[buf][r][i][cc];
+#pragma unroll
+    for (int w = 1; w < S; w *= 2)
+#pragma unroll
+      for (int i = 0; i < S; i += 2 * w) v[i] = make_float2(v[i].x + v[i + w].x, v[i].y + v[i + w].y);
+    return make_float2(v[0].x + fmul(uh, v[0].y), fmul(0.5f * dt, v[0].y));
+  };
   // whether this direction's d_delta store is the last one (the gradient
   // is then complete and, with softplus, taken through it)
   auto dd_final = [&](int dir) { return dir == p.ndir - 1; };
@@ -634,7 +655,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           for (int m = K - 1; m >= 0; --m) {
             if (FULL || m < kcnt) {
               const float4 chv = sCh[SL][m + 1][cl];
-              const float dt = chv.x, hd = chv.y, uh = chv.z, dy = chv.w;
+              const float dt = chv.x, hd = chv.y, dy = chv.w;
               float ddA = 0.f, ddB = 0.f, sBc = 0.f;
 #pragma unroll
               for (int j = 0; j < NPL; ++j) {
@@ -670,27 +691,33 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                 sRed[ONEBAR ? SL : 0][m % KR][0][s * NPL + j][wrow] = reduce_row<S>(fmul(dhb, hd));
                 sRed[ONEBAR ? SL : 0][m % KR][1][s * NPL + j][wrow] = reduce_row<S>(fmul(dy, ht));
               }
-              // d(gate)/d(dt) summed over the lane's states, then over the
-              // channel's lanes with sBc; the channel's S lanes hold identical
-              // totals and store the same value
-              const float dga = reduce_states<S>(ffma(kLn2, ddA, -fmul(kRadPerStep, ddB)));
-              sBc = reduce_states<S>(sBc);
-              const float ddt = dga + fmul(uh, sBc);
-              const float dut = fmul(0.5f * dt, sBc);
-              sDD[ONEBAR ? SL : 0][m][cl] = make_float2(ddt, dut);
+              // d(gate)/d(dt) and sBc summed over the lane's states; their
+              // sums over the channel's lanes are taken from sDD at the
+              // chunk's end
+              sDD[ONEBAR ? SL : 0][m][s][cl] = make_float2(ffma(kLn2, ddA, -fmul(kRadPerStep, ddB)), sBc);
             }
             if (m % KR == 0) {
-              // ONEBAR: with softplus, the factor -expm1(-delta) of each
-              // d_delta element, read while the slot is still this chunk's
-              // (without the second barrier another wave may restage it)
-              float fsp[DPT];
-              if (ONEBAR && m == 0 && p.dsp && dd_final(dir)) {
+              // dt and (dt*u)/2 of each (d_delta, d_u) element this thread
+              // writes, read while the slot is still this chunk's (with
+              // ONEBAR, another wave may restage it after the barrier)
+              float fdt[DPT], fuh[DPT], fsp[DPT];
+              if (m == 0) {
 #pragma unroll
                 for (int k = 0; k < DPT; ++k) {
                   const int e = tid + k * kThreads;
                   const int ee = e < K * CB ? e : 0;
-                  fsp[k] = -expm1f(-sCh[SL][ee / CB + 1][ee % CB].x);
+                  const float4 v = sCh[SL][ee / CB + 1][ee % CB];
+                  fdt[k] = v.x;
+                  fuh[k] = v.z;
                 }
+              }
+              // with softplus, the factor -expm1(-delta) of each d_delta
+              // element; the empty volatile statement keeps this a branch
+              // (executed for every launch if the compiler selected it)
+              if (m == 0 && p.dsp && dd_final(dir)) {
+                asm volatile("");
+#pragma unroll
+                for (int k = 0; k < DPT; ++k) fsp[k] = -expm1f(-fdt[k]);
               }
               // the inputs of chunk ch-1 into the other slot
               if (m == 0 && ch >= 1) stage_store(std::integral_constant<int, 1 - SL>{});
@@ -751,11 +778,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   if constexpr (FAST) {
                     if (e < K * CB && (FULL || e / CB < kcnt)) {
                       const uint32_t o = oD[k] + (uint32_t)ch * stDY;
-                      const float2 v = sDD[ONEBAR ? SL : 0][e / CB][e % CB];
+                      const float2 v = dd_of(ONEBAR ? SL : 0, e / CB, e % CB, fdt[k], fuh[k]);
                       float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
-                      if (p.dsp && dd_final(dir))
-                        dd = ONEBAR ? fmul(dd, fsp[k])
-                                    : softplus_grad_from_delta(dd, sCh[SL][e / CB + 1][e % CB].x);
+                      if (p.dsp && dd_final(dir)) dd = fmul(dd, fsp[k]);
                       store_byte<float>(io.d_delta, o, dd);
                       store_byte<float>(io.d_u, o, dir == 0 ? v.y : pdd[k][1] + v.y);
                     }
@@ -763,12 +788,10 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   }
                   const int64_t idx = dd_index(e, b, dir, i0, kcnt);
                   if (idx >= 0) {
-                    const float2 v = sDD[0][e / CB][e % CB];
+                    const float2 v = dd_of(0, e / CB, e % CB, fdt[k], fuh[k]);
                     float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
                     // with softplus, the complete gradient is taken through it
-                    // (delta of the element: row e / CB + 1 of the slot)
-                    if (p.dsp && dd_final(dir))
-                      dd = softplus_grad_from_delta(dd, sCh[SL][e / CB + 1][e % CB].x);
+                    if (p.dsp && dd_final(dir)) dd = fmul(dd, fsp[k]);
                     io.d_delta[idx] = dd;
                     io.d_u[idx] = dir == 0 ? v.y : pdd[k][1] + v.y;
                   }
