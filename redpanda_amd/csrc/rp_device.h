@@ -154,6 +154,14 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 __device__ __forceinline__ void fill_cos_lin(float2* ctab, int tid) {
   for (int k = tid; k < kTab; k += kThreads) ctab[k] = kCosLin[k];
 }
+// the forward's records with their two expansion coefficients (16 bytes)
+__device__ __forceinline__ float2 cos_lin_coefs(float2 rec);
+__device__ __forceinline__ void fill_cos_lin(float4* ctab, int tid) {
+  for (int k = tid; k < kTab; k += kThreads) {
+    const float2 rec = kCosLin[k], pc = cos_lin_coefs(rec);
+    ctab[k] = make_float4(rec.x, rec.y, pc.x, pc.y);
+  }
+}
 __device__ __forceinline__ void fill_sincos_pairs(float2* cstab, int tid) {
   for (int k = tid; k < kTab; k += kThreads) cstab[k] = kSinCos[k];
 }
@@ -244,10 +252,14 @@ __device__ __forceinline__ int angle_split(float dt, float wh, float& r) {
 //     Its gate is the forward's to within an ulp (the same expansion,
 //     rounded differently).
 // Both return the gate as (b e)(1 + w), b e = e with the sign bit of m.
+// R: the forward's table record, (m, b (-s a)) as float2, or as float4 with
+// the expansion's two record-only coefficients (p3, p2) appended (taken at
+// the table's fill by the same operations, so the gate is bitwise the same)
+template <class R>
 struct GatePart {
-  float e;    // 2^(dt pah)
-  float r;    // angle remainder, |r| <= 1/2 (table steps)
-  float2 cr;  // (m, b (-s a)) of the table angle
+  float e;  // 2^(dt pah)
+  float r;  // angle remainder, |r| <= 1/2 (table steps)
+  R cr;     // the table angle's record
 };
 
 struct GatePartCS {
@@ -261,27 +273,38 @@ __device__ __forceinline__ float signed_by(float e, float m) {
   return __uint_as_float(__float_as_uint(e) | (__float_as_uint(m) & 0x80000000u));
 }
 
-__device__ __forceinline__ GatePart rot_gate_issue(float dt, float pah, float wh, bool imag,
-                                                   const float2* ctab) {
-  GatePart g;
+// cos(a (k + r)) / b - 1 = -|m| + r (t + r ((1 - |m|) kC2 + r t kA3)),
+// t = b (-s a), kA3 = -a^2/6: the coefficients (p3, p2) = (t kA3,
+// (1 - |m|) kC2) of the record (m, t)
+__device__ __forceinline__ float2 cos_lin_coefs(float2 rec) {
+  constexpr float kA3 = -1.0039880779102944e-4f;
+  return make_float2(fmul(rec.y, kA3), ffma(-fabsf(rec.x), kC2, kC2));
+}
+
+template <class R>
+__device__ __forceinline__ GatePart<R> rot_gate_issue(float dt, float pah, float wh, bool imag,
+                                                      const R* ctab) {
+  GatePart<R> g;
   g.e = exp2_hw(fmul(dt, pah));
   if (!imag) {
     g.r = 0.f;
-    g.cr = make_float2(0.f, 0.f);
+    g.cr = R{};
     return g;
   }
   g.cr = ctab[angle_split(dt, wh, g.r)];
   return g;
 }
 
-__device__ __forceinline__ float rot_gate_finish(const GatePart& g, bool imag) {
+template <class R>
+__device__ __forceinline__ float rot_gate_finish(const GatePart<R>& g, bool imag) {
   if (!imag) return g.e;
   const float r = g.r, am = fabsf(g.cr.x);
-  // cos(a (k + r)) / b - 1 = -|m| + r (t + r ((1 - |m|) kC2 + r t kA3)),
-  // t = b (-s a), kA3 = -a^2/6
-  constexpr float kA3 = -1.0039880779102944e-4f;
-  const float p3 = fmul(g.cr.y, kA3), p2 = ffma(-am, kC2, kC2);
-  const float w = ffma(r, ffma(r, ffma(r, p3, p2), g.cr.y), -am);
+  float2 pc;  // (p3, p2)
+  if constexpr (std::is_same<R, float4>::value)
+    pc = make_float2(g.cr.z, g.cr.w);
+  else
+    pc = cos_lin_coefs(g.cr);
+  const float w = ffma(r, ffma(r, ffma(r, pc.x, pc.y), g.cr.y), -am);
   const float be = signed_by(g.e, g.cr.x);
   return ffma(be, w, be);
 }
@@ -342,9 +365,9 @@ __device__ __forceinline__ bool imag_of(bool has_imag) {
 // Gate of state slot j for lane slice s (forward flavour): rotational if
 // n < NR, else the tracking gate pah = tanh(theta) (pad states beyond N
 // carry 0 and B = C = 0).
-template <int S, class GK>
+template <int S, class GK, class R>
 __device__ __forceinline__ float gate_of(int j, int s, int NR, bool has_imag, float dt, float pah,
-                                         float wh, const float2* ctab) {
+                                         float wh, const R* ctab) {
   if (j >= GK::kTJ) return pah;
   const bool imag = imag_of<GK>(has_imag);
   if (j < GK::kRJ) return rot_gate_finish(rot_gate_issue(dt, pah, wh, imag, ctab), imag);
@@ -402,9 +425,9 @@ __device__ __forceinline__ void load_gate_regs(GateRegs<NPL>& gp, const float* A
 //     y = sum_j h_j C_j     (FMA chain in j order).
 // hdu = (dt*u)/2, so hb = hdu*B_n equals beta_t/2 exactly; hbp holds the
 // previous step's hb.  Shared verbatim by the scan and step kernels.
-template <int S, int NPL, class GK>
+template <int S, int NPL, class GK, class R>
 __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
-                                            const GateRegs<NPL>& gp, const float2* ctab, float dt,
+                                            const GateRegs<NPL>& gp, const R* ctab, float dt,
                                             float hdu, const float* __restrict__ Bs,
                                             const float* __restrict__ Cs, int s, int NR,
                                             bool has_imag) {
@@ -426,10 +449,10 @@ __device__ __forceinline__ float fwd_update(float (&h)[NPL], float (&hbp)[NPL],
 // state across steps instead of two, and the same operations on the same
 // values, so the results are bitwise those of fwd_update.  The step's h_j and
 // hb_j are left in hn / hbn for a caller that stores them.
-template <int S, int NPL, class GK>
+template <int S, int NPL, class GK, class R>
 __device__ __forceinline__ float fwd_update_carried(float (&sm)[NPL], float (&hn)[NPL],
                                                     float (&hbn)[NPL], const GateRegs<NPL>& gp,
-                                                    const float2* ctab, float dt, float hdu,
+                                                    const R* ctab, float dt, float hdu,
                                                     const float* __restrict__ Bs,
                                                     const float* __restrict__ Cs, int s, int NR,
                                                     bool has_imag) {

@@ -28,11 +28,22 @@ constexpr int fwd_tb() { return S * NPL > 40 ? kFwdTB / 2 : kFwdTB; }
 // the register budget the compiler is held to, so that VGPRs do not limit
 // the occupancy below what the LDS gives (7 leaves the recurrence of every
 // shape its registers).
+template <int S, int NPL, int REC = 8>
+constexpr int fwd_occupancy_rec() {
+  constexpr int TB = fwd_tb<S, NPL>(), CB = kWaves * (kWave / S), NP = S * NPL;
+  constexpr int lds = TB * CB * 12 + 2 * TB * NP * 4 + kTab * REC;
+  return 163840 / lds < 7 ? 163840 / lds : 7;
+}
+// The gate table's records carry their two expansion coefficients (16
+// bytes: two VALU operations fewer per rotational state-step) where that
+// leaves the occupancy as it is with 8-byte records.
+template <int S, int NPL>
+constexpr bool fwd_wide_rec() {
+  return fwd_occupancy_rec<S, NPL, 16>() == fwd_occupancy_rec<S, NPL, 8>();
+}
 template <int S, int NPL>
 constexpr int fwd_occupancy() {
-  constexpr int TB = fwd_tb<S, NPL>(), CB = kWaves * (kWave / S), NP = S * NPL;
-  constexpr int lds = TB * CB * 12 + 2 * TB * NP * 4 + kTab * 8;
-  return 163840 / lds < 7 ? 163840 / lds : 7;
+  return fwd_occupancy_rec<S, NPL, fwd_wide_rec<S, NPL>() ? 16 : 8>();
 }
 
 // MODEL: the instantiation for the model's launches, whose full blocks take
@@ -50,7 +61,8 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
   __shared__ float sB[TB][NP];     // per step, layout [s*NPL + j] -> state j*S + s
   __shared__ float sC[TB][NP];
   __shared__ float sY[TB][CB];     // the block's y, written out channel-contiguous
-  __shared__ float2 sCos[kTab];      // (m, b (-sin a)) records of the gate table
+  // (m, b (-sin a)) records of the gate table, with their coefficients when wide
+  __shared__ std::conditional_t<fwd_wide_rec<S, NPL>(), float4, float2> sCos[kTab];
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
