@@ -73,8 +73,8 @@ C1_SHAPE = dict(B=8, L=64, D=256, NR=16, NT=0)
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-step", action="store_true", help="skip the step() workload")
     ap.add_argument("--no-long", action="store_true",
