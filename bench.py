@@ -65,6 +65,14 @@ STEP_SHAPE = dict(R=4096, layers=8, D=1024, NR=16, NT=4)
 # Long-sequence causal stress: batch 64, L=2048, d_inner 1024, d_state 64
 # complex plus 8 tracking, fp32 inputs.
 LONG_SHAPE = dict(B=64, L=2048, D=1024, NR=64, NT=8)
+# Launch groups whose HBM bytes are reported as one figure: the scan
+# backward with its two reductions (dB/dC tile partials, float64 parameter
+# partials), and the mixer gate's backward with its dD reduction.  The names
+# are the kernels' short names in the rocprofv3 counter summaries.
+TRAFFIC_SUMS = {
+    "scan_bwd_kernel+reductions": ("scan_bwd_kernel", "bwd_reduce_bc4", "bwd_reduce_par"),
+    "mixer_out_bwd+reduction": ("mixer_out_bwd_vec_kernel", "mixer_out_reduce_kernel"),
+}
 # The reference's CPU configuration: one causal layer, batch 8, L=64, 8 heads
 # x head_dim 32 (d_inner 256), d_state 16 real decay-only, forward only.
 C1_SHAPE = dict(B=8, L=64, D=256, NR=16, NT=0)
@@ -797,12 +805,14 @@ def measured_traffic(name="traffic.json"):
     except (OSError, KeyError, ValueError):
         return {}
     out = {name: v["bytes"] for name, v in k.items()}
-    if "scan_bwd_kernel" in k:
-        out["scan_bwd_kernel+reductions"] = sum(
-            k[n]["bytes"] for n in ("scan_bwd_kernel", "bwd_reduce_bc", "bwd_reduce_par") if n in k)
-    if "mixer_out_bwd_vec_kernel" in k:
-        out["mixer_out_bwd+reduction"] = sum(
-            k[n]["bytes"] for n in ("mixer_out_bwd_vec_kernel", "mixer_out_reduce_kernel") if n in k)
+    for total, parts in TRAFFIC_SUMS.items():
+        if parts[0] in k:
+            # every part must be in the summary: a renamed kernel would
+            # otherwise drop its bytes from the total without a trace
+            missing = [n for n in parts if n not in k]
+            if missing:
+                raise KeyError(f"profiles/{name} lacks {missing} for {total}")
+            out[total] = sum(k[n]["bytes"] for n in parts)
     return out
 
 
