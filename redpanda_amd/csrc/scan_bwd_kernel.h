@@ -12,6 +12,12 @@
 //     dhdu_t = sum_n dhb_t B_t      -> ddt += u/2 dhdu, du = dt/2 dhdu
 //     rot:   dAr += dg dt g,   dAi -= dg dt e sin,   ddt += dg (Ar g - Ai e sin)
 //     track: dTk += dg
+// q_t is formed as fma(g_{t+1}, q_{t+1}, dy_t C_t) and dhb_t as 2 q_t - dy_t
+// C_t: one rounding per step at q's magnitude (fwd_update in rp_device.h has
+// the forward's counterpart and the reason).  The chunk recompute keeps the
+// form h_t = g_t s_{t-1} + hb_t, since dg needs s_{t-1} anyway; it restarts
+// from the forward's checkpoint every kCkptK steps, so its states stay
+// within an ulp or two of the forward's and its roundings do not accumulate.
 //
 // Work split: one workgroup = CB channels x a group of `bg` batch rows, both
 // directions.  The forward stored the state entering every kCkptK-step chunk;
@@ -481,24 +487,32 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 
   for (int b = b_lo; b < b_hi; ++b) {
     for (int dir = 0; dir < p.ndir; ++dir) {
-      // gq: the g_{t+1} q_{t+1} term of q_t;  gr: the term of dhb_t.  They are
-      // equal except at the last step, where an outside consumer of the final
-      // state contributes dh_last to q and 2*dbeta_last to dhb.
-      // (FAST has no final-state gradients: gr equals gq throughout and is
-      // not kept.)
-      float gq[NPL], gr[NPL];
+      // qn, gn: q and g of the step processed before (the next in the
+      // recurrence's time order), so that q_t = fma(g_{t+1}, q_{t+1}, dy_t C_t)
+      // rounds once at q's magnitude (see fwd_update in rp_device.h), and
+      // dhb_t = q_t + g_{t+1} q_{t+1} = 2 q_t - dy_t C_t.  An outside consumer
+      // of the final state (general instantiation, causal) contributes
+      // dh_last to the last step's q (as qn with gn = 1) and 2 * dbeta_last
+      // to its dhb (gr, used at that step only: fin).
+      float qn[NPL], gn[NPL], gr[NPL];
+      bool fin = false;
       if constexpr (FAST) fast_sweep(b, dir);
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
         const int n = j * S + s;
-        gq[j] = 0.f;
+        qn[j] = 0.f;
+        gn[j] = 0.f;
         gr[j] = 0.f;
         if (!FAST && dir == 0 && cvalid && n < p.N) {
           const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
-          if (io.dh_last != nullptr) gq[j] = io.dh_last[idx];
+          if (io.dh_last != nullptr) {
+            qn[j] = io.dh_last[idx];
+            gn[j] = 1.f;
+          }
           if (io.dbeta_last != nullptr) gr[j] = 2.f * io.dbeta_last[idx];
         }
       }
+      if constexpr (!FAST) fin = dir == 0 && (io.dh_last != nullptr || io.dbeta_last != nullptr);
       // parameter-gradient sums over up to kParChunks chunks (fp32), added
       // into the float64 per-thread sums every kParChunks chunks and at the
       // end of the sweep; cpt: the tracking-state sum of a slot decided at
@@ -676,8 +690,12 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   ht = HT[m][j];
                 else
                   ht = ffma(g, SP[m][j], fmul(hd, Bv));
-                const float q = ffma(dy, Cv, gq[j]);
-                const float dhb = q + (FAST ? gq[j] : gr[j]);
+                const float dyc = fmul(dy, Cv);
+                const float q = ffma(gn[j], qn[j], dyc);
+                float dhb = ffma(2.f, q, -dyc);
+                if constexpr (!FAST) {
+                  if (fin) dhb = q + gr[j];
+                }
                 sBc = ffma(dhb, Bv, sBc);
                 const float dg = fmul(q, SP[m][j]);
                 if (j >= GK::kTJ) {  // tracking in every lane
@@ -693,8 +711,8 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   ddA = ffma(j < GK::kRJ ? gp.pah[j] : pam[j], t1, ddA);  // Ar log2(e) dg g
                   ddB = ffma(gp.wh[j], t2, ddB);                          // Ai 256/(2 pi) dg e sin
                 }
-                gq[j] = fmul(g, q);
-                if constexpr (!FAST) gr[j] = gq[j];
+                qn[j] = q;
+                gn[j] = g;
                 // every lane of the row holds the row's total for its slice
                 // s, so the lanes sharing s store the same value
                 sRed[ONEBAR ? SL : 0][m % KR][0][s * NPL + j][wrow] = reduce_row<S>(fmul(dhb, hd));
@@ -704,6 +722,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
               // sums over the channel's lanes are taken from sDD at the
               // chunk's end
               sDD[ONEBAR ? SL : 0][m][s][cl] = make_float2(ffma(kLn2, ddA, -fmul(kRadPerStep, ddB)), sBc);
+              if constexpr (!FAST) fin = false;
             }
             if (m % KR == 0) {
               // dt and (dt*u)/2 of each (d_delta, d_u) element this thread
@@ -874,16 +893,17 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
           one_chunk(ch - 1, std::true_type{}, Slot0{});
         }
       }
-      // after the sweep gq = g_0 q_0: the gradient of the initial state, since
-      // h_0 = g_0 (h0 + beta0/2) + hb_0
+      // after the sweep (qn, gn) = (q_0, g_0), and g_0 q_0 is the gradient of
+      // the initial state, since h_0 = g_0 (h0 + beta0/2) + hb_0
       if (!FAST && dir == 0 && io.d_h0 != nullptr && cvalid) {
 #pragma unroll
         for (int j = 0; j < NPL; ++j) {
           const int n = j * S + s;
           if (n < p.N) {
             const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
-            io.d_h0[idx] = gq[j];
-            io.d_beta0[idx] = 0.5f * gq[j];
+            const float gq = fmul(gn[j], qn[j]);
+            io.d_h0[idx] = gq;
+            io.d_beta0[idx] = 0.5f * gq;
           }
         }
       }

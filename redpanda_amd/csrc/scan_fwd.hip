@@ -113,15 +113,17 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
     asm volatile("" : "+s"(bo), "+s"(to));
   };
   for (int dir = 0; dir < p.ndir; ++dir) {
-    // sm = h + hb of the previous step (of the initial state h0, beta0 / 2)
-    float sm[NPL];
+    // the state h and the previous step's hb (the initial state h0, beta0 / 2)
+    float h[NPL], hb[NPL];
 #pragma unroll
     for (int j = 0; j < NPL; ++j) {
       const int n = j * S + s;
-      sm[j] = 0.f;
+      h[j] = 0.f;
+      hb[j] = 0.f;
       if (dir == 0 && p.h0 != nullptr && cvalid && n < p.N) {
         const int64_t idx = ((int64_t)b * p.D + c) * p.N + n;
-        sm[j] = p.h0[idx] + 0.5f * p.beta0[idx];
+        h[j] = p.h0[idx];
+        hb[j] = 0.5f * p.beta0[idx];
       }
     }
     // the lane's channel-row slot (rh, ci0), its row within a pass in time
@@ -372,9 +374,8 @@ __global__ __launch_bounds__(kThreads, (fwd_occupancy<S, NPL>())) void scan_fwd_
       auto step = [&](int r) {
         const int i = i0 + r;
         const float2 dh = sDH[r][cl];
-        float h[NPL], hb[NPL];
-        float y = fwd_update_carried<S, NPL, GK>(sm, h, hb, gp, sCos, dh.x, dh.y, &sB[r][s * NPL],
-                                                 &sC[r][s * NPL], s, p.NR, has_imag);
+        float y = fwd_update<S, NPL, GK>(h, hb, gp, sCos, dh.x, dh.y, &sB[r][s * NPL],
+                                         &sC[r][s * NPL], s, p.NR, has_imag);
         // the channel's S lanes hold the same total and store the same value
         sY[r][cl] = reduce_states<S>(y);
         if (o.ckpt != nullptr && ((r + 1) % kCkptK) == 0 && i + 1 < L) {

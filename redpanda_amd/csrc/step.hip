@@ -285,8 +285,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       const float hbp = RANK1 ? fmul(hdp, Bp[n]) : 0.5f * bs;
       const float g = gate_of<S, GK>(j, q, p.NR, has_imag, dt, pah[n], wh[n], sCos);
       const float hb = fmul(hd, Bs[n]);
-      const float sm = hs + hbp;
-      hs = ffma(g, sm, hb);
+      hs = ffma(g, hs, ffma(g, hbp, hb));  // fwd_update's form and rounding
       if constexpr (!RANK1) bs = 2.f * hb;
       ys[q] = ffma(hs, Cs[n], ys[q]);
     }
