@@ -102,7 +102,10 @@ typedef struct rp_scan_fwd_out {
  * d_h0, d_beta0: NULL, or (B, D, N) fp32 outputs receiving the gradient of
  * the initial state h0 / beta0 (requires h0).  Deterministic: every sum
  * runs in a fixed order (the float atomic adds some shapes use each update
- * an address that no other thread touches).
+ * an address that no other thread touches).  work must be ordinary device
+ * memory (hipMalloc, or a tensor of torch's caching allocator): those
+ * float64 atomic adds run on the device's own atomic units, which HIP does
+ * not guarantee for host-mapped, managed or fine-grained allocations.
  */
 typedef struct rp_scan_bwd_io {
   const float* dy;
@@ -401,7 +404,9 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream);
  * streams, host threads, parallel graph branches) race and must be
  * serialised.  Every partial is written before it is read, so nothing needs
  * clearing between calls.  The scratch is looked up on the stream's device
- * on the first call there.
+ * on the first call there; that first call may itself be made under HIP
+ * graph capture (the launches are captured, the lookup is not a stream
+ * operation).
  */
 #define RP_SCAN_BWD_SCRATCH_BYTES (64ll << 20)
 int rp_scan_bwd_noalloc(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream);

@@ -170,7 +170,7 @@ def step_core_ref(delta, u, Bc, Cc, A_real, A_imag, track, D, state):
     gates = parts[0] if len(parts) == 1 else torch.cat(parts, dim=-1)
     beta_t = (delta * u).unsqueeze(-1) * Bc.unsqueeze(1)
     if state is None:
-        h = torch.zeros(batch, d_inner, Bc.shape[-1], dtype=beta_t.dtype)
+        h = torch.zeros(batch, d_inner, Bc.shape[-1], dtype=beta_t.dtype, device=beta_t.device)
         beta_prev = torch.zeros_like(beta_t)
     else:
         h, beta_prev = state
@@ -210,8 +210,9 @@ def scan_sequential(delta, u, Bc, Cc, Ar, Ai, Tk, h0=None, beta0=None, reverse=F
     delta, u, Bc, Cc, Ar, Ai, Tk = map(f, (delta, u, Bc, Cc, Ar, Ai, Tk))
     batch, L, d_inner = u.shape
     n = Bc.shape[-1]
-    h = torch.zeros(batch, d_inner, n, dtype=torch.float64) if h0 is None else f(h0)
-    bp = torch.zeros(batch, d_inner, n, dtype=torch.float64) if beta0 is None else f(beta0)
+    z64 = dict(dtype=torch.float64, device=u.device)
+    h = torch.zeros(batch, d_inner, n, **z64) if h0 is None else f(h0)
+    bp = torch.zeros(batch, d_inner, n, **z64) if beta0 is None else f(beta0)
     ys = [None] * L
     order = range(L - 1, -1, -1) if reverse else range(L)
     for t in order:
@@ -241,7 +242,8 @@ def scan_adjoint(delta, u, Bc, Cc, Ar, Ai, Tk, dy, reverse=False):
     order = list(range(L - 1, -1, -1)) if reverse else list(range(L))
     # forward sweep: keep every h_t (float64, small shapes only)
     hs, betas, gs = {}, {}, {}
-    h = torch.zeros(batch, d_inner, n, dtype=torch.float64)
+    z64 = dict(dtype=torch.float64, device=u.device)
+    h = torch.zeros(batch, d_inner, n, **z64)
     bp = torch.zeros_like(h)
     prev = None
     for t in order:
@@ -250,14 +252,14 @@ def scan_adjoint(delta, u, Bc, Cc, Ar, Ai, Tk, dy, reverse=False):
         h = g * h + 0.5 * beta + 0.5 * g * bp
         hs[t], betas[t], gs[t] = h, beta, g
         bp = beta
-    zeros = torch.zeros(batch, d_inner, n, dtype=torch.float64)
+    zeros = torch.zeros(batch, d_inner, n, **z64)
     d_delta = torch.zeros_like(delta)
     d_u = torch.zeros_like(u)
     d_B = torch.zeros_like(Bc)
     d_C = torch.zeros_like(Cc)
-    d_Ar = torch.zeros(d_inner, nr, dtype=torch.float64)
-    d_Ai = torch.zeros(d_inner, nr, dtype=torch.float64)
-    d_Tk = torch.zeros(d_inner, n - nr, dtype=torch.float64)
+    d_Ar = torch.zeros(d_inner, nr, **z64)
+    d_Ai = torch.zeros(d_inner, nr, **z64)
+    d_Tk = torch.zeros(d_inner, n - nr, **z64)
     gq_next = zeros          # g_{t+1} q_{t+1}
     for k in range(L - 1, -1, -1):
         t = order[k]

@@ -1,0 +1,292 @@
+"""Every benchmark configuration checked for values at its own full size.
+
+The parity bars are those of the scan tests: forward <= 1e-5 and gradients
+<= 1e-6 (norm-wise, max|a-b| / max|b| per tensor) against the oracle's fp32
+restatement of the reference, with the float64 recurrence as the arbiter
+where the reference's own fp32 error exceeds the bar (`within_bar`).
+
+The HIP kernels run on each configuration's whole grid.  The oracle checks it
+where it can afford to, using the independence the recurrence gives:
+  * batch rows are independent, so a whole row (every channel, every time
+    step) is checked against the oracle run on that row alone: y, d_delta,
+    d_u, and dB / dC, whose sums run over that row's channels;
+  * channels are independent, so a tile of channels of every row is checked
+    against the oracle run on those channels alone: y, d_delta, d_u of every
+    row and the parameter gradients (sums over every row and time step).
+The first and last batch rows and the first and last channel tiles are
+taken, so the largest offsets of every buffer (the long sequence's 9.7 GB
+checkpoint workspace among them) are read back and compared.
+
+Configurations (d_state additive: rotational + tracking):
+  C1  B=8,   L=64,   d_inner 256,  N=16 real decay, causal forward (+ grads)
+  C2  B=256, L=64,   d_inner 1536, N=32+8, bf16 storage, bidirectional forward
+  C3  C2 plus the backward
+  C4  4096 rollouts x 8 layers, d_model 512, N=16+4, mimo_p 2: 32 plies of
+      step() against the full causal forward
+  C5  B=64,  L=2048, d_inner 1024, N=64+8, fp32, causal forward + backward
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import model_ref, scan_ref
+from tests import hip_capi
+from tests.test_gpu_scan import make_case
+
+pytestmark = pytest.mark.gpu
+dev = "cuda"
+FWD_TOL = 1e-5
+GRAD_TOL = 1e-6
+STEP_TOL = 1e-6
+NAMES = ("delta", "u", "Bc", "Cc", "Ar", "Ai", "Tk")
+
+
+def rel(a, b):
+    return scan_ref.rel_err(a.detach(), b.detach())
+
+
+def within_bar(e_hip_ref, e_hip_64, e_ref_64, tol):
+    """Within `tol` of the reference, or, where the reference's own fp32
+    error exceeds `tol`, no further from float64 than it is."""
+    return e_hip_ref <= tol or e_hip_64 <= max(tol, e_ref_64)
+
+
+def _sub(c, rows=None, chans=None):
+    """The case restricted to batch rows and / or channels, on the GPU."""
+    out = dict(c)
+    r = slice(None) if rows is None else rows
+    ch = slice(None) if chans is None else chans
+    for k in ("delta", "u", "dy"):
+        out[k] = c[k][r][:, :, ch].to(dev)
+    for k in ("Bc", "Cc"):
+        out[k] = c[k][r].to(dev)
+    for k in ("Ar", "Ai", "Tk"):
+        out[k] = None if c[k] is None else c[k][ch].to(dev)
+    return out
+
+
+def _oracle(c, bidirectional):
+    """fp32 restatement (forward and autograd gradients; chunks recomputed in
+    backward to bound memory) and the float64 recurrence with its adjoint,
+    on whatever device the case lives on."""
+    f = lambda t: None if t is None else t.float()
+    leaves = [None if c[k] is None else f(c[k]).clone().requires_grad_(True) for k in NAMES]
+    dl, uu, Bc, Cc, Ar, Ai, Tk = leaves
+    y, _ = scan_ref.contracted_scan_ref(dl, uu, Bc, Cc, Ar, Ai, Tk, c["N"], checkpoint=True)
+    if bidirectional:
+        yr, _ = scan_ref.contracted_scan_ref(dl.flip(1), uu.flip(1), Bc.flip(1), Cc.flip(1),
+                                             Ar, Ai, Tk, c["N"], checkpoint=True)
+        y = y + yr.flip(1)
+    (y * c["dy"].float()).sum().backward()
+    g32 = {k: (None if t is None else t.grad) for k, t in zip(NAMES, leaves)}
+    args = [c[k] for k in NAMES]
+    y64, _, _ = scan_ref.scan_sequential(*args)
+    g64 = scan_ref.scan_adjoint(*args, c["dy"])
+    if bidirectional:
+        y64 = y64 + scan_ref.scan_sequential(*args, reverse=True)[0]
+        gr = scan_ref.scan_adjoint(*args, c["dy"], reverse=True)
+        g64 = {k: (None if v is None else v + gr[k]) for k, v in g64.items()}
+    return y.detach(), g32, y64, g64
+
+
+def _compare(tag, hip, ref32, ref64, keys):
+    """(name, hip-ref, hip-f64, ref-f64, bar) rows for the named tensors."""
+    rows = []
+    for k in keys:
+        h, r, r64 = hip[k], ref32[k], ref64[k]
+        if r is None:
+            continue
+        h = h.to(r.device)
+        rows.append((f"{tag}:{k}", rel(h, r), rel(h, r64), rel(r, r64),
+                     FWD_TOL if k == "y" else GRAD_TOL))
+    return rows
+
+
+def _check_full_grid(c, bidirectional, rows, chans, label, record):
+    y, g = hip_capi.scan_fwd_bwd(c, bidirectional)
+    hip = dict(g, y=y)
+    table = []
+    for b in rows:
+        sc = _sub(c, rows=slice(b, b + 1))
+        y32, g32, y64, g64 = _oracle(sc, bidirectional)
+        h = {k: hip[k][b:b + 1] for k in ("y", "delta", "u", "Bc", "Cc")}
+        table += _compare(f"row {b}", h, dict(g32, y=y32), dict(g64, y=y64),
+                          ("y", "delta", "u", "Bc", "Cc"))
+        del sc, y32, g32, y64, g64
+        torch.cuda.empty_cache()
+    for lo, hi in chans:
+        sc = _sub(c, chans=slice(lo, hi))
+        y32, g32, y64, g64 = _oracle(sc, bidirectional)
+        h = {k: hip[k][:, :, lo:hi] for k in ("y", "delta", "u")}
+        h.update({k: None if hip[k] is None else hip[k][lo:hi] for k in ("Ar", "Ai", "Tk")})
+        table += _compare(f"ch {lo}-{hi - 1}", h, dict(g32, y=y32), dict(g64, y=y64),
+                          ("y", "delta", "u", "Ar", "Ai", "Tk"))
+        del sc, y32, g32, y64, g64
+        torch.cuda.empty_cache()
+    bad = [r for r in table if not within_bar(*r[1:])]
+    fw = [r for r in table if r[0].endswith(":y")]
+    gr = [r for r in table if not r[0].endswith(":y")]
+    wf = max(fw, key=lambda r: r[1])
+    wg = max(gr, key=lambda r: r[1])
+    line = (f"{label}: y hip-ref {wf[1]:.1e} (hip-f64 {wf[2]:.1e}, ref-f64 {wf[3]:.1e}); "
+            f"worst grad hip-ref {wg[1]:.1e} ({wg[0]}; hip-f64 {wg[2]:.1e}, ref-f64 "
+            f"{wg[3]:.1e}); {len(table)} tensors, {len(bad)} outside")
+    print(line, flush=True)
+    record("parity", line)
+    assert not bad, f"{label}: (tensor, hip-ref, hip-f64, ref-f64, bar) outside: {bad[:6]}"
+    return table
+
+
+def test_c1_real_decay_layer(gpu_lib, record_property):
+    """C1, the reference's own CPU configuration: batch 8, L=64, 8 heads x 32
+    (d_inner 256), d_state 16 real decay only, A = -exp(U(log 1, log 16)),
+    causal.  The whole grid against the oracle: forward, and the gradients
+    as well."""
+    c = make_case(1001, B=8, L=64, D=256, NR=16, NT=0, complex_=False, ar_hi=math.log(16.0))
+    assert c["Ai"] is None and c["Tk"] is None
+    y, g = hip_capi.scan_fwd_bwd(c, False)
+    sc = _sub(c)
+    y32, g32, y64, g64 = _oracle(sc, False)
+    table = _compare("C1", dict(g, y=y), dict(g32, y=y32), dict(g64, y=y64),
+                     ("y", "delta", "u", "Bc", "Cc", "Ar"))
+    bad = [r for r in table if not within_bar(*r[1:])]
+    ey = table[0]
+    wg = max(table[1:], key=lambda r: r[1])
+    line = (f"C1 B=8 L=64 D=256 N=16 real, causal (whole grid): y hip-ref {ey[1]:.1e} "
+            f"(hip-f64 {ey[2]:.1e}, ref-f64 {ey[3]:.1e}); worst grad hip-ref {wg[1]:.1e} "
+            f"({wg[0]}; hip-f64 {wg[2]:.1e}, ref-f64 {wg[3]:.1e})")
+    print(line, flush=True)
+    record_property("parity", line)
+    # the forward, which is what C1 measures, is held to the bar without the
+    # float64 allowance
+    assert ey[1] <= FWD_TOL, line
+    assert not bad, bad
+
+
+def test_c2_c3_eval_shape_full_grid(gpu_lib, record_property):
+    """C2 / C3 at the full Eval-Mamba grid: B=256, L=64, d_inner 1536,
+    d_state 32 + 8, bf16-stored inputs, bidirectional forward + backward.
+    Rows 0 and 255 whole; channel tiles 0-31 and 1504-1535 of every row."""
+    c = make_case(1003, B=256, L=64, D=1536, NR=32, NT=8, dtype=torch.bfloat16)
+    _check_full_grid(c, True, rows=(0, 255), chans=((0, 32), (1504, 1536)),
+                     label="C2/C3 B=256 L=64 D=1536 N=40 bf16, bidirectional (full grid)",
+                     record=record_property)
+
+
+def test_c5_long_sequence_full_grid(gpu_lib, record_property):
+    """C5 at its full grid: B=64, L=2048, d_inner 1024, d_state 64 + 8, fp32,
+    causal forward + backward (a 9.7 GB checkpoint workspace).  Rows 0 and
+    63 whole; channel tiles 0-15 and 1008-1023 of every row."""
+    c = make_case(1005, B=64, L=2048, D=1024, NR=64, NT=8)
+    _check_full_grid(c, False, rows=(0, 63), chans=((0, 16), (1008, 1024)),
+                     label="C5 B=64 L=2048 D=1024 N=72 fp32, causal (full grid)",
+                     record=record_property)
+
+
+# ─── C4: the batched step at 4096 rollouts ──────────────────────────────────
+
+SEARCH = dict(d_model=512, n_layer=8, d_state=20, n_track_state=4, mimo_p=2, vocab_size=64)
+CORE_ROWS = (0, 1, 1000, 2047, 2048, 3071, 4094, 4095)
+
+
+class _CoreTap:
+    """Records, on chosen plies, the SSM core's arguments and results of every
+    layer's fused step (redpanda_amd.mamba.hip_step) for a few rollouts."""
+
+    def __init__(self, plies, rows):
+        import redpanda_amd.mamba as hm
+        self.hm, self.plies, self.rows = hm, set(plies), torch.tensor(rows, device=dev)
+        self.ply, self.calls = 0, []
+
+    def __enter__(self):
+        self.orig = self.hm.hip_step
+
+        def tap(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, **kw):
+            y, st = self.orig(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state, **kw)
+            if self.ply in self.plies:
+                r = self.rows
+                pick = lambda t: None if t is None else t.index_select(0, r).clone()
+                self.calls.append(dict(
+                    ply=self.ply, x_dt=pick(delta), u=pick(u), Bc=pick(Bc), Cc=pick(Cc),
+                    Ar=A_real, Ai=A_imag, Tk=track, D=Dskip, z=pick(kw.get("z")),
+                    state=None if state is None else tuple(pick(s) for s in state),
+                    y=pick(y), h=pick(st[0]), beta=pick(st[1])))
+            return y, st
+
+        self.hm.hip_step = tap
+        return self
+
+    def __exit__(self, *exc):
+        self.hm.hip_step = self.orig
+
+
+def _core_rows(calls, D):
+    """(layer/ply tag, hip-ref, hip-f64, ref-f64) for y, h, beta of every
+    recorded SSM core against oracle.scan_ref.step_core_ref."""
+    from redpanda_amd.step import full_beta, is_compact
+    import torch.nn.functional as F
+    out = []
+    for cl in calls:
+        st = cl["state"]
+        if st is not None and is_compact(st[1]):
+            st = (st[0], full_beta(st[1], D))
+        beta = full_beta(cl["beta"], D) if is_compact(cl["beta"]) else cl["beta"]
+        delta = F.softplus(cl["x_dt"].float())
+        gate = F.silu(cl["z"]) if cl["z"] is not None else None
+        args = (delta, cl["u"], cl["Bc"], cl["Cc"], cl["Ar"], cl["Ai"], cl["Tk"], cl["D"])
+        y32, (h32, b32) = scan_ref.step_core_ref(*args, st)
+        d = lambda t: None if t is None else t.double()
+        y64, (h64, b64) = scan_ref.step_core_ref(*map(d, args),
+                                                 None if st is None else tuple(map(d, st)))
+        if gate is not None:
+            y32, y64 = y32 * gate, y64 * gate.double()
+        tag = f"ply {cl['ply']} layer {cl['layer']}"
+        for k, a, r, r64 in (("y", cl["y"], y32, y64), ("h", cl["h"], h32, h64),
+                             ("beta", beta, b32, b64)):
+            out.append((f"{tag} {k}", rel(a, r), rel(a, r64), rel(r, r64)))
+    return out
+
+
+@pytest.mark.parametrize("compact", [False, True], ids=["full-cache", "rank1-cache"])
+def test_c4_search_step_4096_rollouts(gpu_lib, record_property, compact):
+    """C4 at full size: 4096 rollouts through 8 causal layers (d_model 512,
+    d_state 16 + 4, mimo_p 2), one N(0, 1) move embedding per rollout per
+    ply, 32 plies of Mamba.step(input_embed=...) against
+    Mamba.forward(input_embeds=(4096, 32, 512)) on every rollout (1e-6),
+    with the reference's cache format and with rank-1 beta rows; and each
+    layer's SSM core of the first and last ply against the oracle's step
+    (oracle.scan_ref.step_core_ref) on 8 rollouts, first and last included."""
+    from tests.test_gpu_model import _pair
+    hip, _ = _pair(SEARCH, seed=6)
+    hip.eval()
+    R, T = 4096, 32
+    gen = torch.Generator().manual_seed(1004)
+    emb = torch.randn(R, T, SEARCH["d_model"], generator=gen).to(dev)
+    with torch.no_grad():
+        full = hip(None, input_embeds=emb)
+        cache, outs = None, []
+        with _CoreTap((0, T - 1), CORE_ROWS) as tap:
+            for t in range(T):
+                tap.ply = t
+                hdn, cache = hip.step(input_embed=emb[:, t], cache=cache, compact=compact)
+                outs.append(hdn)
+        steps = torch.stack(outs, 1)
+        e_all = rel(steps, full)
+        e_ply = max(rel(steps[:, t], full[:, t]) for t in range(T))
+    assert len(tap.calls) == 2 * SEARCH["n_layer"]
+    for i, cl in enumerate(tap.calls):
+        cl["layer"] = i % SEARCH["n_layer"]
+    D = 2 * SEARCH["d_model"]
+    core = _core_rows(tap.calls, D)
+    bad = [r for r in core if not within_bar(*r[1:], STEP_TOL)]
+    worst = max(core, key=lambda r: r[1])
+    line = (f"C4 R=4096 x 8 layers, 32 plies ({'rank-1' if compact else 'full'} cache): "
+            f"step vs forward {e_all:.1e} (worst ply {e_ply:.1e}); SSM core vs oracle step "
+            f"on {len(CORE_ROWS)} rollouts, plies 0 and 31, all layers: worst {worst[1]:.1e} "
+            f"({worst[0]}; hip-f64 {worst[2]:.1e}, ref-f64 {worst[3]:.1e}), {len(bad)} outside")
+    print(line, flush=True)
+    record_property("parity", line)
+    assert e_all <= STEP_TOL and e_ply <= STEP_TOL, line
+    assert not bad, bad[:6]

@@ -323,3 +323,61 @@ def test_final_state_gradients(gpu_lib):
     for k in names:
         e = rel(lv[k].grad, lv64[k].grad)
         assert e <= 2e-6, f"{k}: {e:.3e}"
+
+
+# ─── whole-tile fast paths against the partial-tile path, bit for bit ───────
+
+def _lanes_per_channel(N):
+    return 4 if N <= 20 else (8 if N <= 40 else 16)
+
+
+STORAGE = {
+    # (delta / u storage, B / C storage, softplus on load); the last two take
+    # the forward's instantiation for the model's launches
+    "fp32": (torch.float32, torch.float32, False),
+    "bf16": (torch.bfloat16, torch.bfloat16, False),
+    "fp16": (torch.float16, torch.float16, False),
+    "model-bf16": (torch.bfloat16, torch.float32, True),
+    "model-fp16": (torch.float16, torch.float32, True),
+}
+
+
+@pytest.mark.parametrize("N,NT", [(20, 4), (40, 8), (72, 8)])
+@pytest.mark.parametrize("storage", sorted(STORAGE))
+@pytest.mark.parametrize("bidir", [False, True])
+def test_whole_tile_paths_equal_partial_tile(gpu_lib, N, NT, storage, bidir):
+    """Channels are independent, so a launch over D = CB channels (one whole
+    tile: the forward's fast staging of full blocks, and the backward's
+    whole-tile instantiation) and one over D = CB - 1 (a partial tile: the
+    element-wise staging and the general backward) must give the first CB - 1
+    channels the same bits: y; for causal scans the final state; d_delta,
+    d_u and the parameter gradients, each a per-channel sum in a fixed order
+    (dB / dC sum over channels and are left out).  L = 70 covers full blocks
+    and a tail; storage types, directions and the softplus-on-load delta
+    cache (read back by the reverse direction) as the kernels take them."""
+    dt_in, dt_bc, softplus = STORAGE[storage]
+    CB = 4 * (64 // _lanes_per_channel(N))
+    c = make_case(600 + N, B=3, L=70, D=CB, NR=N - NT, NT=NT)
+    if softplus:
+        c["delta"] = torch.randn(c["delta"].shape, generator=torch.Generator().manual_seed(6)) - 2
+    c["delta"], c["u"] = c["delta"].to(dt_in), c["u"].to(dt_in)
+    c["Bc"], c["Cc"] = c["Bc"].to(dt_bc), c["Cc"].to(dt_bc)
+    part = dict(c)
+    for k in ("delta", "u", "dy"):
+        part[k] = c[k][:, :, :CB - 1].contiguous()
+    for k in ("Ar", "Ai", "Tk"):
+        part[k] = c[k][:CB - 1].contiguous()
+    y1, g1 = hip_capi.scan_fwd_bwd(c, bidir, softplus=softplus)
+    y2, g2 = hip_capi.scan_fwd_bwd(part, bidir, softplus=softplus)
+    same = lambda a, b: torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert same(y1[:, :, :CB - 1].contiguous(), y2), "y"
+    for k in ("delta", "u"):
+        assert same(g1[k][:, :, :CB - 1].contiguous(), g2[k]), k
+    for k in ("Ar", "Ai", "Tk"):
+        assert same(g1[k][:CB - 1].contiguous(), g2[k]), k
+    if not bidir:
+        _, _, (h1, b1), keep1 = hip_capi.scan_fwd(c, with_state=True, softplus=softplus)
+        _, _, (h2, b2), keep2 = hip_capi.scan_fwd(part, with_state=True, softplus=softplus)
+        torch.cuda.synchronize()
+        assert same(h1[:, :CB - 1].contiguous().cpu(), h2.cpu()), "h_last"
+        assert same(b1[:, :CB - 1].contiguous().cpu(), b2.cpu()), "beta_last"

@@ -101,3 +101,20 @@ def test_noalloc_refuses_a_shape_beyond_the_scratch(gpu_lib):
     st = lib.rp_scan_bwd_noalloc(ctypes.byref(a), ctypes.byref(io), _lib.stream_of("cuda"))
     assert st == -4
     assert b"static scratch holds" in lib.rp_last_error()
+
+
+def test_noalloc_first_call_under_graph_capture(gpu_lib):
+    """The first call of a process, captured into a HIP graph (the use the
+    entry point is for), replayed four times with other allocation-free
+    calls between the replays: bit for bit rp_scan_bwd's every time.  A
+    child process, so the captured call is the process's first (the one that
+    looks the scratch up)."""
+    import os
+    import subprocess
+    import sys
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_graph_capture.py")
+    r = subprocess.run([sys.executable, "-u", script], capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-3000:], r.stderr[-3000:], flush=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    assert r.stdout.strip().endswith("ok")
