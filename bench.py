@@ -272,10 +272,11 @@ def bench_scan(torch, args, dtype):
                 t_inf=t_inf, fwd_bytes=fb, bwd_bytes=bb, T=B * L)
 
 
-def bench_step(torch, args, layers=None, plies=32, keep=True):
+def bench_step(torch, args, layers=None, plies=32, keep=True, R=None):
     from redpanda_amd import _lib
     sh = STEP_SHAPE
-    R, D, NR, NT = sh["R"], sh["D"], sh["NR"], sh["NT"]
+    R = sh["R"] if R is None else R
+    D, NR, NT = sh["D"], sh["NR"], sh["NT"]
     layers = sh["layers"] if layers is None else layers
     N = NR + NT
     dev = torch.device("cuda:0")
@@ -383,12 +384,12 @@ def bench_step(torch, args, layers=None, plies=32, keep=True):
 PLY_SHAPE = dict(R=4096, layers=8, d_model=512, d_state=20, n_track=4, mimo_p=2)
 
 
-def bench_ply(torch, args, plies=8):
+def bench_ply(torch, args, plies=8, R=None, graphs=False):
     """Whole plies through Mamba.step(input_embed=...) (projections on
     hipBLASLt, norms, the fused step kernel per layer), fp32, no autograd:
     the reference's cache format and rank-1 beta rows."""
     from redpanda_amd import mamba as hm
-    sh = PLY_SHAPE
+    sh = dict(PLY_SHAPE) if R is None else dict(PLY_SHAPE, R=R)
     dev = torch.device("cuda:0")
     torch.manual_seed(0)
     cfg = hm.MambaConfig(d_model=sh["d_model"], n_layer=sh["layers"], d_state=sh["d_state"],
@@ -410,6 +411,142 @@ def bench_ply(torch, args, plies=8):
             dt = (time.perf_counter() - t0) / plies
             out[name] = dict(s_per_ply=dt, rollout_steps_s=sh["R"] / dt)
             del cache
+            if graphs:
+                # the same plies replayed from HIP graphs (StepGraph)
+                from redpanda_amd.step_graph import StepGraph
+                sg = StepGraph(model, sh["R"], compact=compact, embed=True)
+                for k in range(2):
+                    sg(input_embed=emb[k])
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for k in range(plies):
+                    sg(input_embed=emb[k])
+                torch.cuda.synchronize()
+                dt = (time.perf_counter() - t0) / plies
+                out[name + "_graph"] = dict(s_per_ply=dt, rollout_steps_s=sh["R"] / dt)
+                del sg
+    return out
+
+
+# Rollout counts of the step sweep: MARS advances survivors x simulations
+# rollouts per ply (sim_budget 64 by default), and its diagnostics sweep the
+# batched step over 1 to 512 (engine/mars_search.py:59,
+# engine/mars_diagnostics.py:169-227); 4096 is the headline workload.
+STEP_SWEEP_R = (1, 8, 32, 128, 512, 4096)
+
+
+def bench_step_sweep(torch, args):
+    """The step kernel (full and rank-1 caches, 8 layers per ply) and the
+    whole ply through Mamba.step at each rollout count of STEP_SWEEP_R."""
+    rows = []
+    for R in STEP_SWEEP_R:
+        st = bench_step(torch, args, plies=16, R=R)
+        ply = bench_ply(torch, args, plies=8, R=R, graphs=True)
+        rows.append({
+            "R": R,
+            "step_kernel": {"avg_launch_s": st["t_launch"], "GBps": st["GBps"],
+                            "frac": st["GBps"] / HBM_PEAK_GBS,
+                            "rollout_steps_s": R / (st["t_launch"] * STEP_SHAPE["layers"])},
+            "step_kernel_rank1": {"avg_launch_s": st["t_launch_rank1"], "GBps": st["GBps_rank1"],
+                                  "frac": st["GBps_rank1"] / HBM_PEAK_GBS,
+                                  "rollout_steps_s":
+                                      R / (st["t_launch_rank1"] * STEP_SHAPE["layers"])},
+            "whole_ply": {"s_per_ply": ply["full"]["s_per_ply"],
+                          "rollout_steps_s": ply["full"]["rollout_steps_s"]},
+            "whole_ply_rank1": {"s_per_ply": ply["rank1"]["s_per_ply"],
+                                "rollout_steps_s": ply["rank1"]["rollout_steps_s"]},
+            "whole_ply_graph": {"s_per_ply": ply["full_graph"]["s_per_ply"],
+                                "rollout_steps_s": ply["full_graph"]["rollout_steps_s"]},
+            "whole_ply_rank1_graph": {"s_per_ply": ply["rank1_graph"]["s_per_ply"],
+                                      "rollout_steps_s": ply["rank1_graph"]["rollout_steps_s"]},
+        })
+        print(f"[bench] step sweep R={R}: kernel {st['t_launch'] * 1e6:.1f} us/launch "
+              f"(rank-1 {st['t_launch_rank1'] * 1e6:.1f}); whole ply "
+              f"{ply['full']['s_per_ply'] * 1e3:.3f} ms (rank-1 "
+              f"{ply['rank1']['s_per_ply'] * 1e3:.3f}); from graphs "
+              f"{ply['full_graph']['s_per_ply'] * 1e3:.3f} ms (rank-1 "
+              f"{ply['rank1_graph']['s_per_ply'] * 1e3:.3f})", file=sys.stderr, flush=True)
+    return rows
+
+
+# Training through step() (SearchMamba.dynamics_rollout, the DynamicsTrainer's
+# forward, engine/search_mamba.py:252-273, engine/train.py:558): the search
+# model of the step workload (8 causal layers, d_model 512, d_state 16 + 4,
+# mimo_p 2), the trainer's batch of 64 boards, a 64-token board prefix and
+# 8 move plies (max_pv, engine/train.py:491).
+DYN_SHAPE = dict(B=64, L_board=64, T=8, d_model=512, layers=8, d_state=20, n_track=4,
+                 mimo_p=2, vocab=8192, eval_dim=512)
+
+
+def bench_dynamics(torch, args, reps=10):
+    """Forward + backward of SearchMamba.dynamics_rollout (prime_cache over the
+    board, then T differentiable steps with the value, continuation and
+    consistency heads), fp32 and under bf16 autocast; also the prime_cache
+    part alone, so that the T steps' share is the difference."""
+    from redpanda_amd.search_mamba import SearchMamba, SearchMambaConfig
+    sh = DYN_SHAPE
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    cfg = SearchMambaConfig(d_model=sh["d_model"], n_layer=sh["layers"], d_state=sh["d_state"],
+                            n_track_state=sh["n_track"], mimo_p=sh["mimo_p"],
+                            vocab_size=sh["vocab"])
+    model = SearchMamba(cfg, vocab_size=sh["vocab"], eval_dim=sh["eval_dim"]).to(dev).train()
+    gen = torch.Generator(device=dev).manual_seed(1012)
+    board = torch.randint(0, sh["vocab"], (sh["B"], sh["L_board"]), generator=gen, device=dev)
+    moves = torch.randint(0, sh["vocab"], (sh["B"], sh["T"]), generator=gen, device=dev)
+
+    def full():
+        v, c, f = model.dynamics_rollout(board, moves)
+        (v.float().sum() + c.float().mean() + f.float().pow(2).mean()).backward()
+
+    def prime():
+        fin, _ = model.backbone.prime_cache(board)
+        fin.float().pow(2).mean().backward()
+
+    timer = EventTimer(torch)
+    out = {}
+    for name, amp in (("fp32", None), ("bf16_autocast", torch.bfloat16)):
+        ctx = (lambda: torch.autocast("cuda", dtype=amp)) if amp else None
+        res = {}
+        for part, fn in (("train_step", full), ("prime_only", prime)):
+            def run(fn=fn):
+                model.zero_grad(set_to_none=True)
+                if ctx is None:
+                    fn()
+                else:
+                    with ctx():
+                        fn()
+            for _ in range(3):
+                run()
+            torch.cuda.synchronize()
+            res[part + "_s"] = timer.time(run, reps)
+        res["steps_share_s"] = res["train_step_s"] - res["prime_only_s"]
+        res["boards_s"] = sh["B"] / res["train_step_s"]
+        out[name] = res
+    # the fp32 forward + backward captured with torch.cuda.make_graphed_callables
+    # (replayed from HIP graphs: the host's launch work taken out)
+
+    class Rollout(torch.nn.Module):
+        def __init__(self, m):
+            super().__init__()
+            self.m = m
+
+        def forward(self, b, mv):
+            return self.m.dynamics_rollout(b, mv)
+
+    graphed = torch.cuda.make_graphed_callables(Rollout(model), (board, moves),
+                                                allow_unused_input=True)
+
+    def run_graphed():
+        model.zero_grad(set_to_none=True)
+        v, c, f = graphed(board, moves)
+        (v.float().sum() + c.float().mean() + f.float().pow(2).mean()).backward()
+
+    for _ in range(3):
+        run_graphed()
+    torch.cuda.synchronize()
+    out["fp32_graphed"] = {"train_step_s": timer.time(run_graphed, reps)}
+    out["fp32_graphed"]["boards_s"] = sh["B"] / out["fp32_graphed"]["train_step_s"]
     return out
 
 
@@ -1201,6 +1338,16 @@ def main():
               f"{ply['full']['s_per_ply'] * 1e3:.3f} ms ({ply['full']['rollout_steps_s']:.4g} "
               f"rollout-steps/s); rank-1 cache {ply['rank1']['s_per_ply'] * 1e3:.3f} ms "
               f"({ply['rank1']['rollout_steps_s']:.4g})", file=sys.stderr, flush=True)
+    sweep = dyn = None
+    if not args.no_step:
+        sweep = bench_step_sweep(torch, args)
+        dyn = bench_dynamics(torch, args)
+        print(f"[bench] dynamics rollout fwd+bwd ({DYN_SHAPE}): fp32 "
+              f"{dyn['fp32']['train_step_s'] * 1e3:.2f} ms (prime part "
+              f"{dyn['fp32']['prime_only_s'] * 1e3:.2f} ms); bf16 autocast "
+              f"{dyn['bf16_autocast']['train_step_s'] * 1e3:.2f} ms; fp32 from graphs "
+              f"{dyn['fp32_graphed']['train_step_s'] * 1e3:.2f} ms",
+              file=sys.stderr, flush=True)
     hbm_practical = practical_hbm_peak(torch)
     print(f"[bench] torch 1 GiB copy: {hbm_practical:.0f} GB/s", file=sys.stderr, flush=True)
     lay = mix = None
@@ -1309,6 +1456,17 @@ def main():
                 "achieved_GBps": step["GBps_rank1"],
                 "frac": step["GBps_rank1"] / HBM_PEAK_GBS,
                 "traffic": tr.get("step_tile_kernel[rank1]")},
+            "sweep": None if sweep is None else {
+                "workload": "the step kernel over 8 layers (d_inner 1024, d_state 16 + 4) and "
+                            "the whole ply through Mamba.step(input_embed) at each rollout count, "
+                            "eager and replayed from HIP graphs (StepGraph); kernel times by HIP "
+                            "events, whole plies by the host clock",
+                "rows": sweep},
+            "training_through_step": None if dyn is None else {
+                "workload": "SearchMamba.dynamics_rollout forward + backward (prime_cache over "
+                            "the board, then differentiable step() plies with the value, "
+                            "continuation and consistency heads); no optimizer",
+                "config": DYN_SHAPE, **dyn},
             "from_shared_state": {
                 "workload": "first ply after a batch-1 cache is fanned out to the rollouts "
                             "(broadcast input state, no copies)",

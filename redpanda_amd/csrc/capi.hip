@@ -544,11 +544,15 @@ int rp_step(const rp_step_args* a, void* stream) {
     // parameters, B / C rows) while keeping many workgroups in flight;
     // measured at 4096 rollouts x 1024 channels, d_state 20: 4 per workgroup
     // (4096 workgroups) beat 1..3 and 6..32 with the full beta; with rank-1
-    // rows (half the bytes per rollout) 8 beat 1..4 and 16
+    // rows (half the bytes per rollout) 8 beat 1..4 and 16.  Below those
+    // caps the count aims at about 512 workgroups, so that fewer rollouts
+    // still amortise the prologue: at 512 rollouts, 4 per workgroup (512
+    // workgroups) take 42 us full / 27 us rank-1, where 1 per workgroup
+    // (2048) took 55 / 47 us
     const int64_t ri_max = a->beta_rank1 ? 8 : 4;
     int64_t ri = step_ri_override();
     if (ri == 0) {
-      ri = (a->R * (int64_t)p.ctiles) / 2048;
+      ri = (a->R * (int64_t)p.ctiles) / 512;
       if (ri < 1) ri = 1;
       if (ri > ri_max) ri = ri_max;
     }

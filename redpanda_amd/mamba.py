@@ -167,7 +167,9 @@ class Mamba3Block(nn.Module):
         storage or its version counter, which every in-place update such as
         an optimizer step or load_state_dict advances): an inference loop of
         step() calls then skips five small kernels per layer."""
-        if record_grad:
+        if record_grad or self.__dict__.get("_gates_in_graph"):
+            # (a captured graph computes them in the graph, so that its
+            # replays follow in-place parameter updates)
             return (*self._compute_A(), self._track_or_none())
         key = tuple((t.data_ptr(), t._version, t.device) for t in self._gate_params())
         hit = self.__dict__.get("_gate_cache")
@@ -284,12 +286,14 @@ class Mamba3Block(nn.Module):
 
     # ── O(1) step (engine/mamba.py:427-498) ──
 
-    def step(self, x_t, state=None, compact=False):
+    def step(self, x_t, state=None, compact=False, out=None):
         """One token for a batch: x_t (B, d_model), state (h, beta) fp32
         (B, d_inner, d_state) or None.  Returns (out (B, d_model), (h, beta)).
         beta may also be in rank-1 rows (B, d_inner + d_state) (see
         forward_with_state); the new state keeps the form of the one given,
-        or with no state the form `compact` asks for."""
+        or with no state the form `compact` asks for.  out: None, or the
+        (h, beta) buffers the new state is written to (inference only; see
+        hip_step), returned as the new state."""
         _need_device(x_t, "step()")
         cfg = self.config
         x_branch, z = self.in_proj(x_t).chunk(2, dim=-1)
@@ -300,6 +304,8 @@ class Mamba3Block(nn.Module):
             (state is not None and any(s.requires_grad for s in state)))
         A_real, A_imag, track = self._gates(grad)
         rank1 = is_compact(state[1]) if state is not None else bool(compact)
+        if grad and out is not None:
+            raise ValueError("step: out buffers are for inference (no autograd graph)")
         if grad:
             # differentiable: a length-1 scan from the cached state (a rank-1
             # beta expanded to its full form first)
@@ -316,7 +322,8 @@ class Mamba3Block(nn.Module):
         else:
             # the gate y * silu(z) is applied by the step kernel
             y, (h, beta) = hip_step(x_dt, x_branch, Bc, Cc, A_real, A_imag, track, self.D,
-                                    state, delta_softplus=True, compact=rank1, z=z)
+                                    state, out=None if out is None else (None, *out),
+                                    delta_softplus=True, compact=rank1, z=z)
         return self.out_proj(y), (h, beta)
 
 
@@ -361,10 +368,12 @@ class Mamba(nn.Module):
         return [None] * len(self.layers)
 
     def step(self, token_id=None, cache=None, input_embed=None, apply_final_norm=True,
-             compact=False):
+             compact=False, out_cache=None):
         """One token through every layer (engine/mamba.py:564-601).  A layer
         with no cached state starts from zero and, with compact=True, returns
-        its beta in rank-1 rows (see Mamba3Block.step)."""
+        its beta in rank-1 rows (see Mamba3Block.step).  out_cache: None, or
+        per-layer (h, beta) buffers the new cache is written to (inference
+        only); it is then the returned cache."""
         assert not self.config.bidirectional, "step() requires a causal model"
         if input_embed is not None:
             x = input_embed
@@ -384,7 +393,8 @@ class Mamba(nn.Module):
             _, xn = hip_add_rmsnorm(x, None, self.layers[0]["norm"].weight,
                                     self.layers[0]["norm"].eps)
             for i, layer in enumerate(self.layers):
-                out, st = layer["mixer"].step(xn, cache[i], compact=compact)
+                out, st = layer["mixer"].step(xn, cache[i], compact=compact,
+                                              out=None if out_cache is None else out_cache[i])
                 new_cache.append(st)
                 nxt = self.layers[i + 1]["norm"] if i + 1 < len(self.layers) else (
                     self.norm_f if apply_final_norm else None)
@@ -394,7 +404,8 @@ class Mamba(nn.Module):
                     x, xn = hip_add_rmsnorm(x, out, nxt.weight, nxt.eps)
             return (xn if apply_final_norm else x), new_cache
         for i, layer in enumerate(self.layers):
-            out, st = layer["mixer"].step(layer["norm"](x), cache[i], compact=compact)
+            out, st = layer["mixer"].step(layer["norm"](x), cache[i], compact=compact,
+                                          out=None if out_cache is None else out_cache[i])
             x = x + out
             new_cache.append(st)
         if apply_final_norm:

@@ -78,7 +78,11 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     F.softplus(x) (engine/mamba.py:300).  beta in rank-1 rows (R, D + N)
     returns rank-1 rows; with no state, `compact` chooses the form returned.
     With the gate branch z (R, D) given, y is returned gated: y * silu(z)
-    (silu rounded to z's dtype, as torch computes it).
+    (silu rounded to z's dtype, as torch computes it).  out: None, or the
+    (y, h_new, beta_new) buffers to write (y may be None): fp32 contiguous,
+    h_new (R, D, N), beta_new in the form of the state; h_new may be the
+    input h itself (updated in place), a rank-1 beta_new may not overlap
+    the input rows.
     """
     lib = _lib.load()
     R, D = u.shape
@@ -100,13 +104,19 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     rank1 = bool(compact)
     if state is not None:
         h_in, beta_in, broadcast, rank1 = _state_pair(state[0], state[1], R, D, N)
+    bshape = (R, D + N) if rank1 else (R, D, N)
     if out is None:
         h_out = torch.empty((R, D, N), dtype=torch.float32, device=dev)
-        beta_out = torch.empty((R, D + N) if rank1 else (R, D, N), dtype=torch.float32,
-                               device=dev)
+        beta_out = torch.empty(bshape, dtype=torch.float32, device=dev)
         y = torch.empty((R, D), dtype=torch.float32, device=dev)
     else:
         y, h_out, beta_out = out
+        if y is None:
+            y = torch.empty((R, D), dtype=torch.float32, device=dev)
+        for name, t, shp in (("y", y, (R, D)), ("h", h_out, (R, D, N)), ("beta", beta_out, bshape)):
+            if (t.shape != shp or t.dtype != torch.float32 or t.device != dev or
+                    not t.is_contiguous()):
+                raise ValueError(f"step: out {name} must be a contiguous fp32 {shp} tensor on {dev}")
     a = _lib.StepArgs()
     a.R, a.D, a.N, a.NR, a.NT = R, D, N, NR, NT
     a.delta, a.delta_sr = delta.data_ptr(), delta.stride(0)
