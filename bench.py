@@ -3,6 +3,7 @@
 and the batched O(1) step (4096 rollouts x 8 layers).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-step] [--no-long]
+                    [--no-sweep] [--no-layer] [--no-mixer] [--no-rollout]
 
 One "step" of the headline workload is one forward + backward of one
 bidirectional scan layer over a batch of 256 boards x 64 tokens, d_inner 1536
@@ -90,6 +91,9 @@ def parse():
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer comparison")
     ap.add_argument("--no-mixer", action="store_true", help="skip the mixer-gate kernels")
     ap.add_argument("--no-rollout", action="store_true", help="skip the rollout-boundary ply")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the step sweep over rollout counts and the training-through-step "
+                         "leg (their thousands of small launches swamp a kernel trace)")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="approximate budget of the CPU baseline sample")
     ap.add_argument("--profile-pass", action="store_true",
@@ -1339,7 +1343,7 @@ def main():
               f"rollout-steps/s); rank-1 cache {ply['rank1']['s_per_ply'] * 1e3:.3f} ms "
               f"({ply['rank1']['rollout_steps_s']:.4g})", file=sys.stderr, flush=True)
     sweep = dyn = None
-    if not args.no_step:
+    if not args.no_step and not args.no_sweep:
         sweep = bench_step_sweep(torch, args)
         dyn = bench_dynamics(torch, args)
         print(f"[bench] dynamics rollout fwd+bwd ({DYN_SHAPE}): fp32 "
