@@ -86,10 +86,12 @@ def _ref_state(cfg_kw, seed, perturb=True):
     return ref.state_dict()
 
 
-def _pair(cfg_kw, seed=0, perturb=True):
-    """(hip model, oracle model) on the GPU with identical weights."""
+def _pair(cfg_kw, seed=0, perturb=True, sd=None):
+    """(hip model, oracle model) on the GPU with identical weights (a seeded
+    reference init, or the given state_dict)."""
     hm = _hip()
-    sd = _ref_state(cfg_kw, seed, perturb)
+    if sd is None:
+        sd = _ref_state(cfg_kw, seed, perturb)
     ref = model_ref.Mamba(model_ref.MambaConfig(**cfg_kw))
     ref.load_state_dict(sd)
     hip = hm.Mamba(hm.MambaConfig(**cfg_kw))
@@ -198,13 +200,18 @@ def _layer_step(blk, x_in, g_out, dtype, amp):
     return res
 
 
-def _teacher_forced(cfg_kw, B, L, seed, tag, record, amp=None):
+def _teacher_forced(cfg_kw, B, L, seed, tag, record, amp=None, sd=None, ids=None,
+                    anchor_control=False):
     """Layer-by-layer parity (see the module docstring): per tensor
     (hip-ref, hip-f64, ref-f64), within_bar with the fp32 bars, or one fp16
-    ulp under fp16 autocast."""
-    hip, ref = _pair(cfg_kw, seed)
+    ulp under fp16 autocast.  sd / ids: given weights and token ids instead
+    of a seeded init and random ids.  anchor_control: the allowance is
+    anchored at the larger of the reference's and the exact-scan control's
+    distances from float64 (see test_golden_model_fixture_same_device)."""
+    hip, ref = _pair(cfg_kw, seed, sd=sd)
     m64 = _f64(cfg_kw, ref.state_dict())
-    ids, dout = _inputs(cfg_kw, B, L, seed)
+    rand_ids, dout = _inputs(cfg_kw, B, L, seed)
+    ids = rand_ids if ids is None else ids.to(dev)
     ins, gouts = _layer_trace(m64, ids, dout)
     rows = []
     ctx = _Fp32Scan() if amp is not None else contextlib.nullcontext()
@@ -220,7 +227,10 @@ def _teacher_forced(cfg_kw, B, L, seed, tag, record, amp=None):
                 tol = (AMP_TOL[amp] if amp is not None else (FWD_TOL if k == "out" else GRAD_TOL))
                 rows.append((f"{i}.{k}", tol, rel(rh[k], rr[k]), rel(rh[k], r64[k]),
                              rel(rr[k], r64[k]), rel(rc[k], r64[k])))
-    bad = [r for r in rows if not within_bar(*r[2:5], r[1])]
+    if anchor_control:
+        bad = [r for r in rows if not within_bar(r[2], r[3], max(r[4], r[5]), r[1])]
+    else:
+        bad = [r for r in rows if not within_bar(*r[2:5], r[1])]
     worst = max(rows, key=lambda r: r[2] / r[1])
     excess = max(rows, key=lambda r: r[3] - r[4])
     geo = math.exp(sum(math.log(r[3] / r[4]) for r in rows) / len(rows))
@@ -450,6 +460,37 @@ def test_golden_model_fixture(gpu_lib, bidir):
                 assert rel(b, g[f"prime_beta{i}"]) <= XDEV_TOL
             nxt, _ = m.step(token_id=ids[:, 20], cache=pc)
             assert rel(nxt, g["prime_next"]) <= XDEV_TOL
+
+
+@pytest.mark.parametrize("bidir", [False, True])
+def test_golden_model_fixture_same_device(gpu_lib, record_property, bidir):
+    """The model fixtures' weights and ids (the reference's own seeded init,
+    engine/mamba.py:503-532, whose rotational gates are half above 1: states
+    that grow along the sequence) on one device, layer by layer: HIP against
+    the oracle's restatement of the reference (pinned bit for bit to the
+    fixture on the CPU, tests/test_oracle.py), float64 as the arbiter, the
+    fp32 bars, with an N(0, 1) upstream gradient (the fixture's own loss,
+    mean(norm_f(x)^2), is a near-cancellation whose gradients are rounding
+    residues for any fp32 run).  This makes the cross-device fixture check
+    above a parity check.  Layer by layer, because with growing states the
+    first layer's gradients amplify whatever the later layers hand back: end
+    to end its A gradients sit ~1e-6 from float64 for HIP and ~5e-8 for the
+    reference by that sensitivity, while on the same inputs HIP's are closer
+    to float64 than the reference's.  With growing states every fp32 run's
+    gradients are several 1e-6 from float64, and how close the reference
+    lands on a given tensor is partly chance: the exact-scan control (the
+    same fp32 layer with its scan evaluated in float64, i.e. no scan error at
+    all) lands up to 13x further than the reference on some.  So here the
+    allowance is anchored at the larger of the reference's and the control's
+    distances: HIP is within the bar of the reference, or no further from
+    float64 than an error-free scan's fp32 layer plus the bar."""
+    g = load_golden(f"model_bi{int(bidir)}")
+    kw = dict(d_model=16, n_layer=2, d_state=12, n_track_state=4, mimo_p=2, vocab_size=64,
+              bidirectional=bidir)
+    sd = {k[3:]: v for k, v in g.items() if k.startswith("sd.")}
+    B, L = g["ids"].shape
+    _teacher_forced(kw, B, L, 19, f"model fixture bidir={int(bidir)} (reference init)",
+                    record_property, sd=sd, ids=g["ids"], anchor_control=True)
 
 
 def test_model_step_equals_forward(gpu_lib):
