@@ -159,8 +159,14 @@ __device__ __forceinline__ void store_stream(float4* p, float4 v) {
 // DSP: delta holds x and the step uses softplus(x).
 // RANK1: beta travels as rows [dt*u | B] (D + N floats per rollout); only
 // h moves through the LDS block, and beta_prev = (dt*u)_prev * B_prev.
-template <int S, int NPL, class GK, bool FULLD, bool DSP, bool RANK1>
+// SHARED (whole tiles only): every rollout starts from the one input state
+// (ssr == 0).  Its blocks are read with plain loads, which L2 keeps for the
+// other rollouts, where a rollout's own block is read once with streaming
+// loads: from a shared state 1.65x faster (4096 rollouts: 144 against
+// 237 us); for per-rollout states plain loads were 3-7 % slower.
+template <int S, int NPL, class GK, bool FULLD, bool DSP, bool RANK1, bool SHARED>
 __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
+  static_assert(FULLD || !SHARED, "the shared-state instantiation is for whole tiles");
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
   constexpr int TCH = kStepTile;
@@ -242,8 +248,8 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       for (int m = 0; m < NV; ++m) {
         const int k = tid + m * TCH;
         if (FULLD || k < nvalid) {
-          hl[m] = load_stream(hi4 + k);
-          if constexpr (!RANK1) bl[m] = load_stream(bi4 + k);
+          hl[m] = SHARED ? hi4[k] : load_stream(hi4 + k);
+          if constexpr (!RANK1) bl[m] = SHARED ? bi4[k] : load_stream(bi4 + k);
         }
       }
 #pragma unroll
@@ -321,12 +327,15 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 template <int S, int NPL, class GK, bool DSP, bool RANK1>
 static hipError_t launch_step_tile_d(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ctiles * p.rgroups));
-  if (p.D % kStepTile == 0)
-    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1>), grid, dim3(kThreads), 0,
-                       st, p);
+  if (p.D % kStepTile == 0 && p.ssr == 0)
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1, true>), grid,
+                       dim3(kThreads), 0, st, p);
+  else if (p.D % kStepTile == 0)
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1, false>), grid,
+                       dim3(kThreads), 0, st, p);
   else
-    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false, DSP, RANK1>), grid, dim3(kThreads), 0,
-                       st, p);
+    hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, false, DSP, RANK1, false>), grid,
+                       dim3(kThreads), 0, st, p);
   return hipGetLastError();
 }
 
