@@ -51,9 +51,10 @@ def _template_args(kernel_name):
 
 def short_name(kernel_name):
     """`void rp::scan_bwd_kernel<8, 5, ...>(rp::ScanParams, ...)` -> `scan_bwd_kernel`.
-    The step tile kernel's rank-1 instantiation (last template argument
-    RANK1 = true) is `step_tile_kernel[rank1]`, so the two forms' counters
-    stay apart."""
+    The step tile kernel's rank-1 instantiation (template argument RANK1,
+    the sixth, true) is `step_tile_kernel[rank1]`, and its shared-state
+    instantiation (SHARED, the seventh) carries `[shared]`, so the forms'
+    counters stay apart."""
     name = kernel_name
     depth, out = 0, []
     for ch in name:  # drop template arguments
@@ -68,8 +69,10 @@ def short_name(kernel_name):
     name = re.sub(r"^.*::", "", name)
     if name == "step_tile_kernel":
         args = _template_args(kernel_name)
-        if len(args) == 6 and args[-1] in ("true", "1"):
+        if len(args) >= 6 and args[5] in ("true", "1"):
             name += "[rank1]"
+        if len(args) >= 7 and args[6] in ("true", "1"):
+            name += "[shared]"
     return name
 
 

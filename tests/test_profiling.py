@@ -18,10 +18,12 @@ def test_short_name():
                                 "(rp::ScanParams, rp::BwdIO)") == "scan_bwd_kernel"
     assert profiling.short_name("rp::bwd_reduce_bc(float const*, float*)") == "bwd_reduce_bc"
     # the step tile kernel's two beta forms stay apart
-    full = "void rp::step_tile_kernel<4, 5, rp::GateKind<4, 1, 4>, true, false, false>(rp::StepParams)"
-    rank1 = "void rp::step_tile_kernel<4, 5, rp::GateKind<4, 1, 4>, true, true, true>(rp::StepParams)"
+    full = "void rp::step_tile_kernel<4, 5, rp::GateKind<4, 1, 4>, true, false, false, false>(rp::StepParams)"
+    rank1 = "void rp::step_tile_kernel<4, 5, rp::GateKind<4, 1, 4>, true, true, true, false>(rp::StepParams)"
+    shared = "void rp::step_tile_kernel<4, 5, rp::GateKind<4, 1, 4>, true, false, false, true>(rp::StepParams)"
     assert profiling.short_name(full) == "step_tile_kernel"
     assert profiling.short_name(rank1) == "step_tile_kernel[rank1]"
+    assert profiling.short_name(shared) == "step_tile_kernel[shared]"
 
 
 def test_traffic_scales_by_the_calibration_dispatch(tmp_path):
