@@ -167,10 +167,13 @@ class Mamba3Block(nn.Module):
         storage or its version counter, which every in-place update such as
         an optimizer step or load_state_dict advances): an inference loop of
         step() calls then skips five small kernels per layer."""
-        if record_grad or self.__dict__.get("_gates_in_graph"):
-            # (a captured graph computes them in the graph, so that its
-            # replays follow in-place parameter updates)
+        if record_grad:
             return (*self._compute_A(), self._track_or_none())
+        fixed = self.__dict__.get("_gates_fixed")
+        if fixed is not None:
+            # buffers that a captured graph reads (StepGraph refreshes them
+            # from this method's values whenever a gate parameter changes)
+            return fixed
         key = tuple((t.data_ptr(), t._version, t.device) for t in self._gate_params())
         hit = self.__dict__.get("_gate_cache")
         if hit is not None and hit[0] == key:

@@ -10,13 +10,18 @@ once and replays it: every launch of the ply is issued by one graph launch.
 
 The state lives in two static cache sets that the two captured graphs use in
 turn (graph 0 reads set 0 and writes set 1, graph 1 the reverse), so a ply
-moves the state once, as the eager step does.  The values are those of
-Mamba.step with the same inputs and state (the same kernels in the same
-order); the returned hidden rows and cache are the graph's buffers, valid
-until the next call (clone them to keep them).  Inference only (no autograd
-graph is recorded).  The graphs read the model's parameters in place, so an
-in-place update (an optimizer step, load_state_dict) reaches the next
-replay; a model moved or re-created needs a new StepGraph.
+moves the state once, as the eager step does.  The gates (A_real, A_imag,
+tanh(theta)) depend on the parameters only: the graphs read them from static
+buffers, which a call refreshes outside the graph, with the eager step's
+own values, when a gate parameter has changed (its storage or version
+counter); computing them inside the graph took seven small kernels per
+layer in every replay.  The values are those of Mamba.step with the same
+inputs and state (the same kernels in the same order); the returned hidden
+rows and cache are the graph's buffers, valid until the next call (clone
+them to keep them).  Inference only (no autograd graph is recorded).  The
+graphs read the model's parameters in place, so an in-place update (an
+optimizer step, load_state_dict) reaches the next replay; a model moved or
+re-created needs a new StepGraph.
 """
 
 import torch
@@ -55,17 +60,36 @@ class StepGraph:
                       for _ in range(cfg.n_layer)] for _ in range(2)]
         self.cur = 0
         self.graphs, self.hidden = [], []
-        # the gates are computed inside the graph (not taken from the eager
-        # step's cache), so replays follow in-place parameter updates as the
-        # GEMM weights do
-        for layer in model.layers:
-            layer["mixer"].__dict__["_gates_in_graph"] = True
+        # static gate buffers per layer, read by the graphs
+        self.mixers = [layer["mixer"] for layer in model.layers]
+        with torch.no_grad():
+            self.gates = [tuple(None if g is None else g.detach().clone() for g in mx._gates(False))
+                          for mx in self.mixers]
+        self.gate_key = self._gate_key()
+        for mx, g in zip(self.mixers, self.gates):
+            mx.__dict__["_gates_fixed"] = g
         try:
             self._capture(dev, warmup)
         finally:
-            for layer in model.layers:
-                layer["mixer"].__dict__.pop("_gates_in_graph", None)
+            for mx in self.mixers:
+                mx.__dict__.pop("_gates_fixed", None)
         self.reset()
+
+    def _gate_key(self):
+        return tuple((t.data_ptr(), t._version) for mx in self.mixers for t in mx._gate_params())
+
+    def _refresh_gates(self):
+        """The static gate buffers from the eager step's values, when a gate
+        parameter has changed since they were filled."""
+        key = self._gate_key()
+        if key == self.gate_key:
+            return
+        with torch.no_grad():
+            for mx, bufs in zip(self.mixers, self.gates):
+                for b, g in zip(bufs, mx._gates(False)):
+                    if b is not None:
+                        b.copy_(g)
+        self.gate_key = key
 
     def _capture(self, dev, warmup):
         side = torch.cuda.Stream(device=dev)
@@ -125,6 +149,7 @@ class StepGraph:
         if x.shape != self.inp.shape:
             raise ValueError(f"StepGraph: input {tuple(x.shape)} must be {tuple(self.inp.shape)}")
         self.inp.copy_(x)
+        self._refresh_gates()
         k = self.cur
         self.graphs[k].replay()
         self.cur = 1 - k
