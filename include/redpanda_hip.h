@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 11
+#define RP_ABI_VERSION 12
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -419,6 +419,19 @@ int rp_step_check(const rp_step_args* a);
  * Mamba3Block.step between the projections (engine/mamba.py:466-494).
  */
 int rp_step(const rp_step_args* a, void* stream);
+
+/*
+ * The step with its B / C rows taken from the raw x_proj projections: the
+ * BCNorm + p-sum of rp_bcnorm_fwd (engine/mamba.py:297-300, :336-337)
+ * followed by rp_step (engine/mamba.py:466-494), the same values as those
+ * two calls.  bn->T must be a->R, bn->N the step's d_state, and a->Bc /
+ * a->Cc must be bn->Bc / bn->Cc with row stride N: with one rollout per
+ * workgroup (small batches) the step kernel computes the rows in its
+ * prologue and leaves those buffers unwritten, otherwise rp_bcnorm_fwd
+ * writes them ahead of the step.  One launch fewer per layer where launches
+ * dominate (a Mamba.step ply at MARS's batch sizes).
+ */
+int rp_step_bcnorm(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream);
 
 #ifdef __cplusplus
 }

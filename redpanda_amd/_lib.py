@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -134,6 +134,7 @@ SIGNATURES = {
     "rp_bcnorm_work_bytes": (_i64, [ctypes.POINTER(BcNormArgs)]),
     "rp_bcnorm_fwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), _vp]),
     "rp_bcnorm_bwd": (ctypes.c_int, [ctypes.POINTER(BcNormArgs), ctypes.POINTER(BcNormGrad), _vp]),
+    "rp_step_bcnorm": (ctypes.c_int, [ctypes.POINTER(StepArgs), ctypes.POINTER(BcNormArgs), _vp]),
     "rp_rmsnorm_check": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs)]),
     "rp_rmsnorm_fwd": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs), _vp]),
     "rp_ply_topk_check": (ctypes.c_int, [ctypes.POINTER(PlyTopkArgs)]),

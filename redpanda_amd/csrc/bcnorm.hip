@@ -24,14 +24,6 @@ namespace rp {
 
 namespace {
 
-constexpr int kBcMaxP = 8;
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m);
-  return v;
-}
-
 __device__ __forceinline__ float round_dt(float v, int dtype) {
   if (dtype == RP_F32) return v;
   if (dtype == RP_BF16) {
@@ -81,32 +73,13 @@ __global__ __launch_bounds__(kThreads) void bcnorm_fwd_kernel(BcNormParams p) {
   for (int64_t t = t0 + w; t < t1; t += kWaves) {
 #pragma unroll
     for (int part = 0; part < 2; ++part) {
-      const void* x = p.x[part];
-      float v[SL][kBcMaxP];
-      float ss = 0.f;
+      float acc[SL];
+      bcnorm_token<SL>(p.x[part], t * p.xs[part], p.dt_x, lane, p.N, p.P, p.normalize, p.eps, invK,
+                       wt[part], acc);
 #pragma unroll
       for (int s = 0; s < SL; ++s) {
         const int n = lane + s * kWave;
-#pragma unroll
-        for (int q = 0; q < kBcMaxP; ++q) {
-          v[s][q] = (n < p.N && q < p.P) ? load_in(x, t * p.xs[part] + n * p.P + q, p.dt_x) : 0.f;
-          ss += v[s][q] * v[s][q];
-        }
-      }
-      float r = 1.f;
-      if (p.normalize) r = rsqrtf(wave_sum(ss) * invK + p.eps);
-#pragma unroll
-      for (int s = 0; s < SL; ++s) {
-        const int n = lane + s * kWave;
-        if (n >= p.N) continue;
-        float acc = 0.f;
-#pragma unroll
-        for (int q = 0; q < kBcMaxP; ++q) {
-          if (q >= p.P) break;
-          const float y = p.normalize ? (v[s][q] * r) * wt[part][s][q] : v[s][q];
-          acc = q == 0 ? y : acc + y;
-        }
-        p.out[part][t * p.N + n] = acc;
+        if (n < p.N) p.out[part][t * p.N + n] = acc[s];
       }
     }
   }

@@ -492,9 +492,25 @@ int rp_step_check(const rp_step_args* a) {
   return RP_OK;
 }
 
-int rp_step(const rp_step_args* a, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// rp_step, and with bn the B / C rows from the raw projections: computed in
+// the tile kernel's prologue when it takes one rollout per workgroup (small
+// batches, where a launch saved is worth most), else by the BCNorm kernel
+// into bn->Bc / bn->Cc (= a->Bc / a->Cc) ahead of the step.
+int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
   int st = rp_step_check(a);
   if (st != RP_OK) return st;
+  if (bn != nullptr) {
+    st = rp_bcnorm_check(bn);
+    if (st != RP_OK) return st;
+    if (bn->T != a->R || bn->N != a->N)
+      return fail(RP_ERR_INVALID, "step bcnorm: T must be R and N the step's d_state");
+    if (bn->Bc != a->Bc || bn->Cc != a->Cc || a->Bc_sr != a->N || a->Cc_sr != a->N)
+      return fail(RP_ERR_INVALID, "step bcnorm: a->Bc / a->Cc must be bn->Bc / bn->Cc, row stride N");
+  }
   if (a->R == 0 || a->D == 0) return RP_OK;
   int S = 0, NPL = 0;
   rp::choose_shape((int)a->N, &S, &NPL);
@@ -562,9 +578,36 @@ int rp_step(const rp_step_args* a, void* stream) {
     if ((int64_t)p.ctiles * p.rgroups > kI32Max)
       return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   }
+  if (bn != nullptr && tile && p.ri == 1) {
+    p.bn_fused = 1;
+    p.bn_x[0] = bn->B_raw;
+    p.bn_x[1] = bn->C_raw;
+    p.bn_xs[0] = bn->B_sr;
+    p.bn_xs[1] = bn->C_sr;
+    p.bn_dt = bn->dtype_x;
+    p.bn_w[0] = bn->wB;
+    p.bn_w[1] = bn->wC;
+    p.bn_P = (int)bn->P;
+    p.bn_normalize = bn->normalize;
+    p.bn_eps = bn->eps;
+  } else if (bn != nullptr) {
+    st = rp_bcnorm_fwd(bn, stream);
+    if (st != RP_OK) return st;
+  }
   hipError_t e = rp::launch_step(S, NPL, gk, tile, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "step launch");
   return RP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rp_step(const rp_step_args* a, void* stream) { return step_impl(a, nullptr, stream); }
+
+int rp_step_bcnorm(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
+  if (bn == nullptr) return fail(RP_ERR_INVALID, "step bcnorm: NULL bcnorm args");
+  return step_impl(a, bn, stream);
 }
 
 }  // extern "C"

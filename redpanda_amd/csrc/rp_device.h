@@ -83,6 +83,55 @@ __device__ __forceinline__ float load_in(const void* p, int64_t i, int dtype) {
   return cvt_raw(load_raw(p, i, dtype), dtype);
 }
 
+// Features per state of the MIMO projections (P <= kBcMaxP).
+constexpr int kBcMaxP = 8;
+
+// Sum over a wave's 64 lanes (xor butterfly; every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
+// BCNorm + p-sum of one token (engine/mamba.py:89 RMSNorm, :297-300,
+// :336-337) for the states n = lane + 64 s of a wave:
+//     acc[s] = sum_p (x[n,p] r) w[n,p]   (p in order),
+//     r = rsqrt(mean of x^2 over the N*P features + eps),
+// or the plain p-sum when not normalising.  x holds the token's features at
+// row + n * P + p, in storage dtype dt.  One wave per token, every lane
+// taking part; wt: the lane's weights (1 beyond N or P).  The BCNorm kernel
+// and the step kernel's fused prologue both use it, so they give the same
+// bits.
+template <int SL>
+__device__ __forceinline__ void bcnorm_token(const void* x, int64_t row, int dt, int lane, int N,
+                                             int P, bool normalize, float eps, float invK,
+                                             const float (&wt)[SL][kBcMaxP], float (&acc)[SL]) {
+  float v[SL][kBcMaxP];
+  float ss = 0.f;
+#pragma unroll
+  for (int s = 0; s < SL; ++s) {
+    const int n = lane + s * kWave;
+#pragma unroll
+    for (int q = 0; q < kBcMaxP; ++q) {
+      v[s][q] = (n < N && q < P) ? load_in(x, row + n * P + q, dt) : 0.f;
+      ss += v[s][q] * v[s][q];
+    }
+  }
+  float r = 1.f;
+  if (normalize) r = rsqrtf(wave_sum(ss) * invK + eps);
+#pragma unroll
+  for (int s = 0; s < SL; ++s) {
+    float a = 0.f;
+#pragma unroll
+    for (int q = 0; q < kBcMaxP; ++q) {
+      if (q >= P) break;
+      const float y = normalize ? (v[s][q] * r) * wt[s][q] : v[s][q];
+      a = q == 0 ? y : a + y;
+    }
+    acc[s] = a;
+  }
+}
+
 // The raw element type of storage code IT, as load_raw returns it widened.
 template <int IT>
 using RawOf = typename std::conditional<IT == RP_F32, uint32_t, uint16_t>::type;

@@ -88,6 +88,16 @@ struct StepParams {
   int ctiles;   // tile kernel: channel tiles of kStepTile
   int ri;       // tile kernel: rollouts per workgroup
   int rgroups;  // tile kernel: ceil(R / ri)
+  // tile kernel, one rollout per workgroup: the B / C rows computed in the
+  // prologue from the raw projections (BCNorm + p-sum) instead of read
+  int bn_fused;
+  const void* bn_x[2];    // B_raw, C_raw rows (R, N * bn_P), row strides bn_xs
+  int64_t bn_xs[2];
+  int bn_dt;              // their storage dtype
+  const float* bn_w[2];   // (N * bn_P,) norm weights
+  int bn_P;
+  int bn_normalize;
+  float bn_eps;
 };
 
 // The mixer output gate out = (y + k u D) silu(z) over rows = B * L.

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     const int rr = e / (NBC * NP), q = e % (NBC * NP);
     const int64_t r = r_lo + rr;
     bc[k] = 0.f;
-    if (e < nr * NBC * NP) {
+    if (e < nr * NBC * NP && !(p.bn_fused && q < 2 * NP)) {
       if (q < NP)
         bc[k] = p.Bc[r * p.bsr + q];
       else if (q < 2 * NP)
@@ -212,11 +212,30 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
   for (int n = 0; n < NP; ++n) graw[n] = gate_param_load(p.Ar, p.Ai, p.Tk, cld, n, N, p.NR, p.NT, true);
   const float dsk = p.Dskip[cld];
+  if (p.bn_fused) {
+    // the B and C rows of the workgroup's rollout from the raw projections:
+    // BCNorm + p-sum, one wave per row (bcnorm_token, the BCNorm kernel's
+    // arithmetic); its loads are issued behind the prologue's
+    const int lane = tid % kWave, wv = tid / kWave;
+    const float invK = 1.f / (float)(N * p.bn_P);
+    for (int pr = wv; pr < nr * 2; pr += kWaves) {
+      const int rr = pr >> 1, part = pr & 1;
+      float wt[1][kBcMaxP];
+#pragma unroll
+      for (int q = 0; q < kBcMaxP; ++q)
+        wt[0][q] = (p.bn_normalize && lane < N && q < p.bn_P) ? p.bn_w[part][lane * p.bn_P + q] : 1.f;
+      float acc[1];
+      bcnorm_token<1>(p.bn_x[part], (int64_t)(r_lo + rr) * p.bn_xs[part], p.bn_dt, lane, N,
+                      p.bn_P, p.bn_normalize != 0, p.bn_eps, invK, wt, acc);
+      if (lane < N) sBC[rr][part * NP + lane] = acc[0];
+    }
+  }
   fill_cos_lin(sCos, tid);
 #pragma unroll
   for (int k = 0; k < BCPT; ++k) {
     const int e = tid + k * kThreads;
-    if (e < nr * NBC * NP) sBC[e / (NBC * NP)][e % (NBC * NP)] = bc[k];
+    if (e < nr * NBC * NP && !(p.bn_fused && e % (NBC * NP) < 2 * NP))
+      sBC[e / (NBC * NP)][e % (NBC * NP)] = bc[k];
   }
   float pah[NP], wh[NP];
 #pragma unroll

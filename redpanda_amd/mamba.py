@@ -212,6 +212,19 @@ class Mamba3Block(nn.Module):
             Bc, Cc = hip_bcnorm_psum(B_raw, C_raw, None, None, p, normalize=False)
         return self.dt_proj(dt_raw), Bc, Cc
 
+    def _ssm_proj_raw(self, u):
+        """(x_dt, bcnorm): as _ssm_proj_contracted, with BCNorm + the p-sum
+        left to the step (hip_step's bcnorm argument: the raw B / C
+        projections, BCNorm's weights and eps), which gives the same rows."""
+        cfg = self.config
+        n, p = cfg.d_state, cfg.mimo_p
+        dt_raw, B_raw, C_raw = self.x_proj(u).split([cfg.dt_rank, n * p, n * p], dim=-1)
+        if cfg.use_bcnorm:
+            bcn = (B_raw, C_raw, self.b_norm.weight, self.c_norm.weight, p, self.b_norm.eps, True)
+        else:
+            bcn = (B_raw, C_raw, None, None, p, 0.0, False)
+        return self.dt_proj(dt_raw), bcn
+
     # ── scan ──
 
     def _selective_scan_trapezoidal(self, u, delta, A_real, A_imag, B, C, D,
@@ -301,10 +314,14 @@ class Mamba3Block(nn.Module):
         cfg = self.config
         x_branch, z = self.in_proj(x_t).chunk(2, dim=-1)
         x_branch = F.silu(x_branch)
-        x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
         grad = torch.is_grad_enabled() and (
             any(p.requires_grad for p in self.parameters()) or x_t.requires_grad or
             (state is not None and any(s.requires_grad for s in state)))
+        if grad:
+            x_dt, Bc, Cc = self._ssm_proj_contracted(x_branch)
+        else:
+            # BCNorm + the p-sum go into the step (one launch fewer per layer)
+            x_dt, bcn = self._ssm_proj_raw(x_branch)
         A_real, A_imag, track = self._gates(grad)
         rank1 = is_compact(state[1]) if state is not None else bool(compact)
         if grad and out is not None:
@@ -324,9 +341,9 @@ class Mamba3Block(nn.Module):
             y = y * F.silu(z)
         else:
             # the gate y * silu(z) is applied by the step kernel
-            y, (h, beta) = hip_step(x_dt, x_branch, Bc, Cc, A_real, A_imag, track, self.D,
+            y, (h, beta) = hip_step(x_dt, x_branch, None, None, A_real, A_imag, track, self.D,
                                     state, out=None if out is None else (None, *out),
-                                    delta_softplus=True, compact=rank1, z=z)
+                                    delta_softplus=True, compact=rank1, z=z, bcnorm=bcn)
         return self.out_proj(y), (h, beta)
 
 

@@ -67,7 +67,7 @@ def _state_pair(h, b, R, D, N):
 
 
 def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=None,
-             delta_softplus=False, compact=False, z=None):
+             delta_softplus=False, compact=False, z=None, bcnorm=None):
     """One step for R rollouts.
 
     delta, u: (R, D); Bc, Cc: (R, N) (contracted over p); A_real/A_imag:
@@ -82,10 +82,31 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     (y, h_new, beta_new) buffers to write (y may be None): fp32 contiguous,
     h_new (R, D, N), beta_new in the form of the state; h_new may be the
     input h itself (updated in place), a rank-1 beta_new may not overlap
-    the input rows.
+    the input rows.  bcnorm: None, or (B_raw, C_raw, wB, wC, P, eps,
+    normalize), the raw x_proj projections (R, N * P) and BCNorm's weights
+    (engine/mamba.py:297-300), with Bc and Cc None: the step then takes
+    BCNorm + the p-sum itself (rp_step_bcnorm; the values of
+    hip_bcnorm_psum's rows), inside the step kernel at small batches.
     """
     lib = _lib.load()
     R, D = u.shape
+    bn_args = None
+    if bcnorm is not None:
+        from redpanda_amd.bcnorm import _rows as _bn_rows, make_bcnorm_args
+        if Bc is not None or Cc is not None:
+            raise ValueError("step: give either Bc, Cc or bcnorm")
+        B_raw, C_raw, wB, wC, P, eps, normalize = bcnorm
+        if B_raw.shape != C_raw.shape or B_raw.shape[0] != R or B_raw.shape[-1] % P:
+            raise ValueError(f"step: bcnorm projections must be (R, N * P) = ({R}, N * {P})")
+        Bx, Cx = _bn_rows(B_raw), _bn_rows(C_raw)
+        if Cx.dtype != Bx.dtype:
+            Cx = Cx.to(Bx.dtype)
+        wBc = wB.detach().to(torch.float32).contiguous() if normalize else None
+        wCc = wC.detach().to(torch.float32).contiguous() if normalize else None
+        Nb = Bx.shape[-1] // P
+        Bc = torch.empty((R, Nb), dtype=torch.float32, device=u.device)
+        Cc = torch.empty((R, Nb), dtype=torch.float32, device=u.device)
+        bn_args = make_bcnorm_args(Bx, Cx, wBc, wCc, Nb, P, eps, normalize, Bc, Cc)
     N = Bc.shape[-1]
     NR = 0 if A_real is None else A_real.shape[-1]
     NT = 0 if track is None else track.shape[-1]
@@ -140,5 +161,9 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
             a.dtype_z = _lib.DTYPE_CODES[z.dtype]
         except KeyError:
             raise TypeError(f"step: unsupported dtype {z.dtype} for z") from None
-    _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
+    if bn_args is None:
+        _lib.check(lib.rp_step(ctypes.byref(a), _lib.stream_of(dev)), lib)
+    else:
+        _lib.check(lib.rp_step_bcnorm(ctypes.byref(a), ctypes.byref(bn_args), _lib.stream_of(dev)),
+                   lib)
     return y, (h_out, beta_out)

@@ -221,3 +221,52 @@ def test_in_place_state_update(gpu_lib):
         y2 = torch.empty_like(y1)
         hip_step(*p, (h, b), out=(y2, h, b))
     assert torch.equal(y1, y2) and torch.equal(h1, h) and torch.equal(b1, b)
+
+
+@pytest.mark.parametrize("R,D,NR,NT,P,norm,dt,form", [
+    (8, 256, 16, 4, 2, True, torch.float32, "full"),        # one rollout per workgroup: fused
+    (5, 300, 12, 8, 2, True, torch.bfloat16, "rank1"),      # partial channel tile, fused
+    (3, 512, 32, 8, 4, True, torch.float16, "shared"),      # a broadcast state, fused
+    (16, 128, 16, 0, 8, False, torch.float32, "full"),      # plain p-sum, fused
+    (700, 1024, 16, 4, 2, True, torch.float32, "full"),     # several rollouts per workgroup
+    (700, 1024, 16, 4, 2, True, torch.bfloat16, "rank1"),
+    (6, 96, 12, 6, 2, True, torch.float32, "full"),         # d_state 18: the lane kernel
+])
+def test_step_bcnorm_equals_bcnorm_then_step(gpu_lib, R, D, NR, NT, P, norm, dt, form):
+    """rp_step_bcnorm (BCNorm + p-sum of the raw x_proj projections inside the
+    step where it takes one rollout per workgroup, else the BCNorm kernel
+    first) gives the bits of hip_bcnorm_psum followed by rp_step: y, h and
+    beta, in every cache form, with softplus on load and the output gate."""
+    from redpanda_amd.bcnorm import hip_bcnorm_psum
+    from redpanda_amd.step import compact_beta
+    hip_step = _step()
+    N = NR + NT
+    g = torch.Generator(device=dev).manual_seed(R * 7 + D + N)
+    X = (torch.randn(R, 24 + 2 * N * P, device=dev, generator=g) * 2).to(dt)  # an x_proj output
+    B_raw, C_raw = X[:, 24:24 + N * P], X[:, 24 + N * P:]
+    wB = torch.rand(N * P, device=dev, generator=g) + 0.5
+    wC = torch.rand(N * P, device=dev, generator=g) + 0.5
+    x = torch.randn(R, D, device=dev, generator=g) - 2.0
+    u = torch.randn(R, D, device=dev, generator=g)
+    z = torch.randn(R, D, device=dev, generator=g).to(torch.bfloat16)
+    Ar = -torch.exp(torch.rand(D, NR, device=dev, generator=g) * 2) if NR else None
+    Ai = (torch.rand(D, NR, device=dev, generator=g) * 2 - 1) * 3 if NR else None
+    Tk = torch.tanh(torch.randn(D, NT, device=dev, generator=g)) if NT else None
+    Dk = torch.randn(D, device=dev, generator=g)
+    h = torch.randn(1 if form == "shared" else R, D, N, device=dev, generator=g)
+    if form == "rank1":
+        beta = compact_beta(torch.randn(R, D, device=dev, generator=g),
+                            torch.randn(R, N, device=dev, generator=g))
+    else:
+        beta = torch.randn(h.shape, device=dev, generator=g)
+    if form == "shared":
+        h, beta = h.expand(R, D, N), beta.expand(R, D, N)
+    eps = 1e-5
+    with torch.no_grad():
+        Bc, Cc = hip_bcnorm_psum(B_raw, C_raw, wB, wC, P, eps, normalize=norm)
+        y0, (h0, b0) = hip_step(x, u, Bc, Cc, Ar, Ai, Tk, Dk, (h, beta), delta_softplus=True, z=z)
+        y1, (h1, b1) = hip_step(x, u, None, None, Ar, Ai, Tk, Dk, (h, beta), delta_softplus=True,
+                                z=z, bcnorm=(B_raw, C_raw, wB, wC, P, eps, norm))
+    torch.cuda.synchronize()
+    same = lambda a, b: torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert same(y1, y0) and same(h1, h0) and same(b1, b0)
