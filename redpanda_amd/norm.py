@@ -24,7 +24,9 @@ def hip_add_rmsnorm(x, add, w, eps):
     lib = _lib.load()
     if x.stride(-1) != 1:
         x = x.contiguous()
-    wc = w.detach().to(torch.float32).contiguous()
+    wc = w  # only its data pointer is used
+    if w.dtype is not torch.float32 or not w.is_contiguous():
+        wc = w.detach().to(torch.float32).contiguous()
     a = _lib.RmsNormArgs()
     a.rows, a.d, a.eps = R, d, float(eps)
     a.x, a.x_sr = x.data_ptr(), x.stride(0)

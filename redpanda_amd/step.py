@@ -24,14 +24,21 @@ import ctypes
 import torch
 
 from redpanda_amd import _lib
+from redpanda_amd.bcnorm import _rows as _bn_rows, make_bcnorm_args
 
 
+# (the conversions are skipped where a tensor already qualifies: at the
+# batch sizes MARS runs, a step is bound by the host's per-op cost)
 def _f32c(t):
-    return t.to(torch.float32).contiguous()
+    """fp32 contiguous (only the data pointer is used: no autograd)."""
+    if t.dtype is torch.float32 and t.is_contiguous():
+        return t
+    return t.detach().to(torch.float32).contiguous()
 
 
 def _rows(t):
-    t = t.to(torch.float32)
+    if t.dtype is not torch.float32:
+        t = t.to(torch.float32)
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
@@ -58,8 +65,10 @@ def _state_pair(h, b, R, D, N):
     bshape = (R, D + N) if rank1 else (R, D, N)
     if h.shape != (R, D, N) or b.shape != bshape:
         raise ValueError(f"step: state must be h {(R, D, N)} and beta {bshape}")
-    h = h.to(torch.float32)
-    b = b.to(torch.float32)
+    if h.dtype is not torch.float32:
+        h = h.to(torch.float32)
+    if b.dtype is not torch.float32:
+        b = b.to(torch.float32)
     if R > 1 and h.stride(0) == 0 and b.stride(0) == 0 and h[0].is_contiguous() and \
             b[0].is_contiguous():
         return h, b, 1, rank1
@@ -92,7 +101,6 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
     R, D = u.shape
     bn_args = None
     if bcnorm is not None:
-        from redpanda_amd.bcnorm import _rows as _bn_rows, make_bcnorm_args
         if Bc is not None or Cc is not None:
             raise ValueError("step: give either Bc, Cc or bcnorm")
         B_raw, C_raw, wB, wC, P, eps, normalize = bcnorm
@@ -101,8 +109,8 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
         Bx, Cx = _bn_rows(B_raw), _bn_rows(C_raw)
         if Cx.dtype != Bx.dtype:
             Cx = Cx.to(Bx.dtype)
-        wBc = wB.detach().to(torch.float32).contiguous() if normalize else None
-        wCc = wC.detach().to(torch.float32).contiguous() if normalize else None
+        wBc = _f32c(wB) if normalize else None
+        wCc = _f32c(wC) if normalize else None
         Nb = Bx.shape[-1] // P
         Bc = torch.empty((R, Nb), dtype=torch.float32, device=u.device)
         Cc = torch.empty((R, Nb), dtype=torch.float32, device=u.device)
@@ -116,10 +124,10 @@ def hip_step(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, out=Non
         raise ValueError("step: delta/u must be (R, D) and B/C (R, N)")
     dev = u.device
     delta, u, Bc, Cc = (_rows(t) for t in (delta, u, Bc, Cc))
-    Ar = None if A_real is None else _f32c(A_real.detach())
-    Ai = None if A_imag is None else _f32c(A_imag.detach())
-    Tk = None if track is None else _f32c(track.detach())
-    Dk = _f32c(Dskip.detach())
+    Ar = None if A_real is None else _f32c(A_real)
+    Ai = None if A_imag is None else _f32c(A_imag)
+    Tk = None if track is None else _f32c(track)
+    Dk = _f32c(Dskip)
     h_in = beta_in = None
     broadcast = 0
     rank1 = bool(compact)
