@@ -392,3 +392,27 @@ def test_ply_gather_check(lib):
     assert chk(tokens=0x100002) < 0
     assert chk(out=0x100000) < 0
     assert chk(M=0, tokens=None, out=None) == 0
+
+
+def test_step_bcnorm_rules(lib):
+    """rp_step_bcnorm validates both argument sets and their agreement before
+    any launch: T = R, the same d_state, and the step's B / C rows being the
+    BCNorm outputs with row stride N."""
+    a = _step_args(Bc=0x3000000, Cc=0x3100000)
+    bn = _bcnorm_args(T=16, N=20, P=2, B_sr=40, C_sr=40, B_raw=0x1000000, C_raw=0x1000100,
+                      Bc=0x3000000, Cc=0x3100000)
+    assert lib.rp_bcnorm_check(ctypes.byref(bn)) == 0
+    call = lambda a, bn: lib.rp_step_bcnorm(ctypes.byref(a), ctypes.byref(bn), None)
+    assert call(a, _bcnorm_args(**{**{"T": 17, "N": 20, "P": 2, "B_sr": 40, "C_sr": 40},
+                                   "Bc": 0x3000000, "Cc": 0x3100000})) < 0
+    assert "T must be R" in lib.rp_last_error().decode()
+    assert call(a, _bcnorm_args(T=16, N=10, P=4, B_sr=40, C_sr=40, Bc=0x3000000,
+                                Cc=0x3100000)) < 0
+    assert call(_step_args(Bc=0x3000000, Cc=0x3200000), bn) < 0
+    assert "bn->Bc" in lib.rp_last_error().decode()
+    assert call(a, _bcnorm_args(T=16, N=20, P=2, B_sr=39, C_sr=40, Bc=0x3000000,
+                                Cc=0x3100000)) < 0  # BCNorm's own rules
+    assert lib.rp_step_bcnorm(ctypes.byref(a), None, None) < 0
+    # nothing to do, so nothing is launched
+    assert call(_step_args(R=0, Bc=0x3000000, Cc=0x3100000),
+                _bcnorm_args(T=0, N=20, P=2, B_sr=40, C_sr=40, Bc=0x3000000, Cc=0x3100000)) == 0
