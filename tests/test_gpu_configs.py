@@ -206,6 +206,12 @@ class _CoreTap:
         def tap(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state=None, **kw):
             y, st = self.orig(delta, u, Bc, Cc, A_real, A_imag, track, Dskip, state, **kw)
             if self.ply in self.plies:
+                if Bc is None:
+                    # the step took BCNorm + the p-sum of the raw projections
+                    # itself: the BCNorm kernel gives the same rows
+                    from redpanda_amd.bcnorm import hip_bcnorm_psum
+                    Bx, Cx, wB, wC, P, eps, norm = kw["bcnorm"]
+                    Bc, Cc = hip_bcnorm_psum(Bx, Cx, wB, wC, P, eps, normalize=norm)
                 r = self.rows
                 pick = lambda t: None if t is None else t.index_select(0, r).clone()
                 self.calls.append(dict(
