@@ -139,3 +139,42 @@ def test_step_sweep(gpu_lib, case):
     torch.cuda.synchronize()
     assert torch.equal(h1, h0) and torch.equal(full_beta(b1, D), b0)
     assert torch.equal(y1, y0 * F.silu(z))
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_step_bcnorm_sweep(gpu_lib, case):
+    """The step from raw B / C projections (BCNorm + p-sum inside the step, or
+    the BCNorm kernel first, as the batch decides) equals hip_bcnorm_psum
+    followed by the step, bit for bit: d_state 4..72, P 1..8, 1..700 rollouts,
+    every projection dtype, strided projection views, with and without the
+    norm, both beta forms."""
+    rng = random.Random(500 + case)
+    g = torch.Generator(device=dev).manual_seed(50 + case)
+    NR, NT = rng.choice([(4, 0), (12, 4), (16, 4), (32, 8), (36, 4), (64, 8), (6, 2)])
+    N, R, D = NR + NT, rng.choice([1, 3, 64, 200, 700]), rng.choice([32, 100, 256, 1024])
+    P, dt, norm = rng.choice([1, 2, 4, 8]), rng.choice(DTS), rng.random() < 0.8
+    off = rng.choice([0, 3, 32])
+    X = (torch.randn(R, off + 2 * N * P + 5, device=dev, generator=g) * 2).to(dt)
+    B_raw, C_raw = X[:, off:off + N * P], X[:, off + N * P:off + 2 * N * P]
+    wB = torch.rand(N * P, device=dev, generator=g) + 0.5
+    wC = torch.rand(N * P, device=dev, generator=g) + 0.5
+    x = torch.randn(R, D, device=dev, generator=g) - 2
+    u = torch.randn(R, D, device=dev, generator=g)
+    Ar = -torch.exp(torch.rand(D, NR, device=dev, generator=g))
+    Ai = torch.rand(D, NR, device=dev, generator=g) * 3
+    Tk = torch.tanh(torch.randn(D, NT, device=dev, generator=g)) if NT else None
+    Dk = torch.randn(D, device=dev, generator=g)
+    h = torch.randn(R, D, N, device=dev, generator=g)
+    if rng.random() < 0.5:
+        beta = compact_beta(torch.rand(R, D, device=dev, generator=g) * 0.3,
+                            torch.randn(R, N, device=dev, generator=g))
+    else:
+        beta = torch.randn(R, D, N, device=dev, generator=g)
+    with torch.no_grad():
+        Bc, Cc = hip_bcnorm_psum(B_raw, C_raw, wB, wC, P, 1e-5, normalize=norm)
+        y0, (h0, b0) = hip_step(x, u, Bc, Cc, Ar, Ai, Tk, Dk, (h, beta), delta_softplus=True)
+        y1, (h1, b1) = hip_step(x, u, None, None, Ar, Ai, Tk, Dk, (h, beta), delta_softplus=True,
+                                bcnorm=(B_raw, C_raw, wB, wC, P, 1e-5, norm))
+    torch.cuda.synchronize()
+    same = lambda a, b: torch.equal(a.view(torch.int32), b.view(torch.int32))
+    assert same(y1, y0) and same(h1, h0) and same(b1, b0)
