@@ -624,6 +624,30 @@ def test_search_mamba_golden(gpu_lib):
         assert rel(sm.evaluate_lines(b0, moves.to(dev)), g["lines_slow"]) <= XDEV_TOL
 
 
+def test_branch_scoring_cached_equals_full(gpu_lib):
+    """score_branch (prime the board once, then O(1) steps through a line,
+    engine/search_mamba.py:228-240) and evaluate_with_continuation (the board
+    and every line through the full causal scan, :137-146) score the same
+    lines: line values and continuation logits within 1e-5 of each other and
+    of the float64 arbiter's, on the fixture's weights."""
+    g = load_golden("search")
+    sm, arb = _search_pair(g)
+    sm.eval()
+    arb.eval()
+    board, moves = g["board"][0], g["moves"]
+    with torch.no_grad():
+        vals, conts = sm.evaluate_with_continuation(board.to(dev), moves.to(dev))
+        v64, c64 = arb.evaluate_with_continuation(board, moves)
+        _, cache = sm.prime_board(board.to(dev))
+        for i in range(moves.shape[0]):
+            q, cont = sm.score_branch(cache, [int(t) for t in moves[i]])
+            assert abs(q - float(vals[i])) <= 1e-5 * max(1.0, abs(float(vals[i]))), i
+            assert rel(cont, conts[i]) <= 1e-5, i
+            assert abs(q - float(v64[i])) <= 1e-5 * max(1.0, abs(float(v64[i]))), i
+            assert rel(cont, c64[i]) <= 1e-5, i
+    assert rel(vals, v64) <= 1e-5 and rel(conts, c64) <= 1e-5
+
+
 def test_cpu_tensors_are_refused(gpu_lib):
     """No silent CPU path: the SSM core needs device tensors."""
     hm = _hip()
