@@ -648,6 +648,27 @@ def test_branch_scoring_cached_equals_full(gpu_lib):
     assert rel(vals, v64) <= 1e-5 and rel(conts, c64) <= 1e-5
 
 
+def test_block_ssm_entry_matches_reference(gpu_lib):
+    """Mamba3Block.ssm (engine/mamba.py:303-316: projections, gates and the
+    scan with the D skip), with and without the final state, against the
+    oracle block's same composition; and Mamba.init_cache (:560-562)."""
+    cfg = dict(d_model=32, n_layer=2, d_state=12, n_track_state=4, mimo_p=2, vocab_size=64)
+    hip, ref = _pair(cfg, seed=21)
+    hb, rb = hip.layers[1]["mixer"], ref.layers[1]["mixer"]
+    gen = torch.Generator().manual_seed(22)
+    u = torch.randn(3, 19, hb.config.d_inner, generator=gen).to(dev)
+    with torch.no_grad():
+        y = hb.ssm(u)
+        y2, (h2, b2) = hb.ssm(u, return_state=True)
+        delta, B, C = rb._ssm_proj(u)
+        A_real, A_imag = rb._compute_A()
+        yr = rb._scan(u, delta, A_real, A_imag, B, C)
+        yr2, (hr, br) = rb._scan(u, delta, A_real, A_imag, B, C, return_state=True)
+    assert rel(y, yr) <= 1e-5 and rel(y2, yr2) <= 1e-5
+    assert rel(h2, hr) <= 1e-5 and rel(b2, br) <= 1e-5
+    assert hip.init_cache(3, dev) == [None] * cfg["n_layer"]
+
+
 def test_cpu_tensors_are_refused(gpu_lib):
     """No silent CPU path: the SSM core needs device tensors."""
     hm = _hip()
