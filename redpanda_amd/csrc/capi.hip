@@ -555,7 +555,8 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
                     (a->beta_rank1 || (aligned(a->beta_out, 16) &&
                                        (a->h_in == nullptr || aligned(a->beta_in, 16))));
   if (tile) {
-    p.ctiles = (int)((a->D + rp::kStepTile - 1) / rp::kStepTile);
+    const int tch = rp::kStepTile / rp::step_tile_split(S);
+    p.ctiles = (int)((a->D + tch - 1) / tch);
     // rollouts per workgroup: a few amortise the workgroup's prologue (gate
     // parameters, B / C rows) while keeping many workgroups in flight;
     // measured at 4096 rollouts x 1024 channels, d_state 20: 4 per workgroup

@@ -85,7 +85,7 @@ struct StepParams {
   float* beta_out;
   float* y;
   int ntiles;   // lane-layout kernel: channel tiles of CB
-  int ctiles;   // tile kernel: channel tiles of kStepTile
+  int ctiles;   // tile kernel: channel tiles of kStepTile / step_tile_split(S)
   int ri;       // tile kernel: rollouts per workgroup
   int rgroups;  // tile kernel: ceil(R / ri)
   // tile kernel, one rollout per workgroup: the B / C rows computed in the
@@ -190,6 +190,10 @@ hipError_t launch_rmsnorm_fwd(const RmsNormParams& p, hipStream_t st);
 // Channels (one per thread) of the step tile kernel's workgroup, and the
 // most rollouts one of its workgroups walks.
 constexpr int kStepTile = kThreads;
+// Threads per channel of the step tile kernel for S state slices: two for
+// the 8-slice shapes (d_state 24-40), whose states split between them; the
+// tile then holds kStepTile / 2 channels.
+constexpr int step_tile_split(int S) { return S == 8 ? 2 : 1; }
 constexpr int kStepRiMax = 16;
 
 // Chosen lane split for a state dimension N: S lanes per channel holding NPL

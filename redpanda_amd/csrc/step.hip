@@ -169,7 +169,18 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   static_assert(FULLD || !SHARED, "the shared-state instantiation is for whole tiles");
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
-  constexpr int TCH = kStepTile;
+  // SPL threads per channel: with 8 slices (d_state 24-40) a channel's states
+  // split between two adjacent lanes, slices 0-3 and 4-7 (each one float4
+  // per slot), so that the gate parameters and the states of a thread fit
+  // the registers of several waves per SIMD (one thread per channel took
+  // 256 VGPRs, one wave per SIMD, at d_state 32 all rotational)
+  constexpr int SPL = step_tile_split(S);
+  constexpr int SS = S / SPL;           // slices per thread
+  constexpr int NPT = NP / SPL;         // states per thread
+  constexpr int NVT = NV / SPL;         // float4s per thread
+  static_assert(SPL == 1 || SS == 4, "a split thread holds one float4 per slot");
+  constexpr int TCH = kThreads / SPL;   // channels per workgroup
+  constexpr int NB = TCH * NV / kThreads;  // float4s per thread when staging a block
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
   __shared__ float2 sCos[kTab];           // (m, b (-sin a)) records of the gate table
   __shared__ float sBC[kStepRiMax][NBC * NP];  // B, C (B_prev) rows of the workgroup's rollouts
@@ -179,7 +190,8 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   const int tid = threadIdx.x;
   const int tile = blockIdx.x % p.ctiles, rg = blockIdx.x / p.ctiles;
   const int c0 = tile * TCH;
-  const int c = c0 + tid;
+  const int cl = tid / SPL, half = tid % SPL;  // channel in the tile, slice half
+  const int c = c0 + cl;
   const bool cvalid = FULLD || c < p.D;
   const int cld = cvalid ? c : p.D - 1;  // loads stay in bounds; only valid channels store
   const int nvalid = FULLD ? TCH * NV : min(TCH, p.D - c0) * NV;  // float4s of the block
@@ -207,10 +219,13 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
         bc[k] = p.beta_in[r * p.bssr + p.D + (q - 2 * NP)];
     }
   }
-  // the channel's gate parameters stay in registers for all its rollouts
-  GateRaw graw[NP];
+  // state i of this thread: slot i / SS, slice half * SS + i % SS
+  auto st_n = [&](int i) { return (i / SS) * S + half * SS + i % SS; };
+  // the thread's gate parameters stay in registers for all its rollouts
+  GateRaw graw[NPT];
 #pragma unroll
-  for (int n = 0; n < NP; ++n) graw[n] = gate_param_load(p.Ar, p.Ai, p.Tk, cld, n, N, p.NR, p.NT, true);
+  for (int i = 0; i < NPT; ++i)
+    graw[i] = gate_param_load(p.Ar, p.Ai, p.Tk, cld, st_n(i), N, p.NR, p.NT, true);
   const float dsk = p.Dskip[cld];
   if (p.bn_fused) {
     // the B and C rows of the workgroup's rollout from the raw projections:
@@ -237,13 +252,14 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     if (e < nr * NBC * NP && !(p.bn_fused && e % (NBC * NP) < 2 * NP))
       sBC[e / (NBC * NP)][e % (NBC * NP)] = bc[k];
   }
-  float pah[NP], wh[NP];
+  float pah[NPT], wh[NPT];
 #pragma unroll
-  for (int n = 0; n < NP; ++n) gate_param_finish(n, N, p.NR, true, graw[n], pah[n], wh[n]);
+  for (int i = 0; i < NPT; ++i) gate_param_finish(st_n(i), N, p.NR, true, graw[i], pah[i], wh[i]);
 
   // Per rollout: the block's (h, beta) arrive with coalesced streaming loads
   // (thread t moves float4s t, t+256, ...) into LDS; each thread updates its
-  // channel's states there; coalesced streaming stores write the block back.
+  // states of its channel there; coalesced streaming stores write the block
+  // back.
   // Every input is in LDS or registers before the first store, so h_out and
   // beta_out may alias h_in and beta_in (per-rollout states).
   for (int rr = 0; rr < nr; ++rr) {
@@ -262,18 +278,18 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       const int64_t iblk = r * (p.ssr / 4) + (int64_t)c0 * NV;
       const float4* hi4 = reinterpret_cast<const float4*>(p.h_in) + iblk;
       const float4* bi4 = reinterpret_cast<const float4*>(p.beta_in) + iblk;
-      float4 hl[NV], bl[NV];
+      float4 hl[NB], bl[NB];
 #pragma unroll
-      for (int m = 0; m < NV; ++m) {
-        const int k = tid + m * TCH;
+      for (int m = 0; m < NB; ++m) {
+        const int k = tid + m * kThreads;
         if (FULLD || k < nvalid) {
           hl[m] = SHARED ? hi4[k] : load_stream(hi4 + k);
           if constexpr (!RANK1) bl[m] = SHARED ? bi4[k] : load_stream(bi4 + k);
         }
       }
 #pragma unroll
-      for (int m = 0; m < NV; ++m) {
-        const int k = tid + m * TCH;
+      for (int m = 0; m < NB; ++m) {
+        const int k = tid + m * kThreads;
         if (FULLD || k < nvalid) {
           sH[k] = hl[m];
           if constexpr (!RANK1) sBt[k] = bl[m];
@@ -281,41 +297,48 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       }
     } else {
 #pragma unroll
-      for (int m = 0; m < NV; ++m) {
-        sH[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (!RANK1) sBt[tid + m * TCH] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int m = 0; m < NB; ++m) {
+        sH[tid + m * kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (!RANK1) sBt[tid + m * kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
     __syncthreads();  // the block (and, the first time, the table and B / C rows)
-    float4 h4[NV], b4[NV];
+    // the thread's float4 v: the channel's float4 v * SPL + half
+    float4 h4[NVT], b4[NVT];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      h4[v] = sH[tid * NV + v];
-      if constexpr (!RANK1) b4[v] = sBt[tid * NV + v];
+    for (int v = 0; v < NVT; ++v) {
+      h4[v] = sH[cl * NV + v * SPL + half];
+      if constexpr (!RANK1) b4[v] = sBt[cl * NV + v * SPL + half];
     }
     const float* Bs = sBC[rr];
     const float* Cs = sBC[rr] + NP;
     const float* Bp = sBC[rr] + (NBC - 1) * NP;  // B_prev (rank-1 only)
     const float hd = 0.5f * fmul(dt, uu);
-    float ys[S];
+    float ys[SS];
 #pragma unroll
-    for (int q = 0; q < S; ++q) ys[q] = 0.f;
+    for (int q = 0; q < SS; ++q) ys[q] = 0.f;
 #pragma unroll
-    for (int n = 0; n < NP; ++n) {
-      const int j = n / S, q = n % S;
-      float& hs = (&h4[n / 4].x)[n % 4];
-      float& bs = (&b4[n / 4].x)[n % 4];
+    for (int i = 0; i < NPT; ++i) {
+      const int j = i / SS, ql = i % SS;
+      const int n = st_n(i);
+      float& hs = (&h4[i / 4].x)[i % 4];
+      float& bs = (&b4[i / 4].x)[i % 4];
       // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
       // same bits as the product the full form stored
       const float hbp = RANK1 ? fmul(hdp, Bp[n]) : 0.5f * bs;
-      const float g = gate_of<S, GK>(j, q, p.NR, has_imag, dt, pah[n], wh[n], sCos);
+      const float g = gate_of<S, GK>(j, half * SS + ql, p.NR, has_imag, dt, pah[i], wh[i], sCos);
       const float hb = fmul(hd, Bs[n]);
       hs = ffma(g, hs, ffma(g, hbp, hb));  // fwd_update's form and rounding
       if constexpr (!RANK1) bs = 2.f * hb;
-      ys[q] = ffma(hs, Cs[n], ys[q]);
+      ys[ql] = ffma(hs, Cs[n], ys[ql]);
     }
-    if (cvalid) {
-      float yv = tree_sum<S>(ys) + fmul(uu, dsk);
+    // the channel's y: the balanced tree over its S slices, whose top-level
+    // halves are the two threads' trees when split (fp addition commutes, so
+    // both lanes get the same bits)
+    float ysum = tree_sum<SS>(ys);
+    if constexpr (SPL == 2) ysum = ysum + __shfl_xor(ysum, 1);
+    if (cvalid && half == 0) {
+      float yv = ysum + fmul(uu, dsk);
       if (p.z != nullptr) yv = silu_gate(yv, zz, p.dt_z);
       p.y[r * p.D + c] = yv;
       if constexpr (RANK1) p.beta_out[r * (p.D + N) + c] = fmul(dt, uu);
@@ -324,16 +347,16 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       if (tile == 0 && tid < N) p.beta_out[r * (p.D + N) + p.D + tid] = Bs[tid];
     }
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      sH[tid * NV + v] = h4[v];
-      if constexpr (!RANK1) sBt[tid * NV + v] = b4[v];
+    for (int v = 0; v < NVT; ++v) {
+      sH[cl * NV + v * SPL + half] = h4[v];
+      if constexpr (!RANK1) sBt[cl * NV + v * SPL + half] = b4[v];
     }
     __syncthreads();  // the updated block
     float4* ho4 = reinterpret_cast<float4*>(p.h_out) + blk;
     float4* bo4 = reinterpret_cast<float4*>(p.beta_out) + blk;
 #pragma unroll
-    for (int m = 0; m < NV; ++m) {
-      const int k = tid + m * TCH;
+    for (int m = 0; m < NB; ++m) {
+      const int k = tid + m * kThreads;
       if (FULLD || k < nvalid) {
         store_stream(ho4 + k, sH[k]);
         if constexpr (!RANK1) store_stream(bo4 + k, sBt[k]);
@@ -346,10 +369,11 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 template <int S, int NPL, class GK, bool DSP, bool RANK1>
 static hipError_t launch_step_tile_d(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ctiles * p.rgroups));
-  if (p.D % kStepTile == 0 && p.ssr == 0)
+  const int tch = kThreads / step_tile_split(S);
+  if (p.D % tch == 0 && p.ssr == 0)
     hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1, true>), grid,
                        dim3(kThreads), 0, st, p);
-  else if (p.D % kStepTile == 0)
+  else if (p.D % tch == 0)
     hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1, false>), grid,
                        dim3(kThreads), 0, st, p);
   else
