@@ -550,7 +550,8 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
     return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   const int gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
   // the tile kernel moves each channel's (h, beta) as 16-byte vectors
-  const bool tile = a->N % 4 == 0 && S * NPL == a->N && a->N <= 40 && aligned(a->h_out, 16) &&
+  const bool tile = a->N % 4 == 0 && S * NPL == a->N && rp::step_tile_shape(S, NPL) &&
+                    aligned(a->h_out, 16) &&
                     (a->h_in == nullptr || aligned(a->h_in, 16)) &&
                     (a->beta_rank1 || (aligned(a->beta_out, 16) &&
                                        (a->h_in == nullptr || aligned(a->beta_in, 16))));
@@ -579,7 +580,8 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
     if ((int64_t)p.ctiles * p.rgroups > kI32Max)
       return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   }
-  if (bn != nullptr && tile && p.ri == 1) {
+  // (the prologue's BCNorm takes a state per lane: d_state <= 64)
+  if (bn != nullptr && tile && p.ri == 1 && a->N <= rp::kWave) {
     p.bn_fused = 1;
     p.bn_x[0] = bn->B_raw;
     p.bn_x[1] = bn->C_raw;

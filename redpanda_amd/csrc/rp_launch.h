@@ -190,10 +190,14 @@ hipError_t launch_rmsnorm_fwd(const RmsNormParams& p, hipStream_t st);
 // Channels (one per thread) of the step tile kernel's workgroup, and the
 // most rollouts one of its workgroups walks.
 constexpr int kStepTile = kThreads;
-// Threads per channel of the step tile kernel for S state slices: two for
-// the 8-slice shapes (d_state 24-40), whose states split between them; the
-// tile then holds kStepTile / 2 channels.
-constexpr int step_tile_split(int S) { return S == 8 ? 2 : 1; }
+// Threads per channel of the step tile kernel for S state slices: S / 4 from
+// 8 slices up (d_state 24-40 and 48-80), each thread taking 4 slices (one
+// float4 per slot); the tile then holds kStepTile / (S / 4) channels.
+constexpr int step_tile_split(int S) { return S >= 8 ? S / 4 : 1; }
+// Whether the step tile kernel takes the shape (S, NPL) (d_state = S * NPL).
+constexpr bool step_tile_shape(int S, int NPL) {
+  return S * NPL <= 40 || (S == 16 && NPL <= 5);
+}
 constexpr int kStepRiMax = 16;
 
 // Chosen lane split for a state dimension N: S lanes per channel holding NPL
@@ -221,8 +225,8 @@ hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const Bw
                            hipStream_t st);
 hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
                                float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st);
-// `tile`: the thread-per-channel kernel (N == S*NPL, N % 4 == 0, N <= 40,
-// 16-byte aligned state pointers); otherwise the lane-layout kernel.
+// `tile`: the tile kernel (N == S*NPL, N % 4 == 0, step_tile_shape, 16-byte
+// aligned state pointers); otherwise the lane-layout kernel.
 // Bitwise the same.
 hipError_t launch_step(int S, int NPL, int gk, bool tile, const StepParams& p, hipStream_t st);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);

@@ -8,10 +8,11 @@
 //
 // Two kernels, bitwise the same as each other and as the scan:
 //   * step_tile_kernel (the rollout path: d_state == S*NPL, a multiple of 4,
-//     <= 40): a workgroup owns 256 channels and walks a few rollouts.  Per
-//     rollout, the (256 channels x d_state) blocks of h and beta move with
-//     coalesced streaming 16-byte loads and stores through LDS, where one
-//     thread per channel updates its states; the gate parameters stay in
+//     up to 40, or 48 / 64 / 80): a workgroup owns 256 / SPL channels and
+//     walks a few rollouts.  Per rollout, the (channels x d_state) blocks of
+//     h and beta move with coalesced streaming 16-byte loads and stores
+//     through LDS, where SPL threads per channel (1 up to d_state 20, then
+//     one per 4 slices) update its states; the gate parameters stay in
 //     registers and the B / C rows in LDS for all the workgroup's rollouts.
 //     (Moving each channel's 80 contiguous bytes per thread instead costs
 //     ~15% of the bandwidth.)
@@ -169,16 +170,17 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   static_assert(FULLD || !SHARED, "the shared-state instantiation is for whole tiles");
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
-  // SPL threads per channel: with 8 slices (d_state 24-40) a channel's states
-  // split between two adjacent lanes, slices 0-3 and 4-7 (each one float4
-  // per slot), so that the gate parameters and the states of a thread fit
-  // the registers of several waves per SIMD (one thread per channel took
+  // SPL threads per channel: from 8 slices up (d_state 24-40, 48-80) a
+  // channel's states split between S / 4 adjacent lanes, 4 slices each (one
+  // float4 per slot), so that the gate parameters and the states of a thread
+  // fit the registers of several waves per SIMD (one thread per channel took
   // 256 VGPRs, one wave per SIMD, at d_state 32 all rotational)
   constexpr int SPL = step_tile_split(S);
   constexpr int SS = S / SPL;           // slices per thread
   constexpr int NPT = NP / SPL;         // states per thread
   constexpr int NVT = NV / SPL;         // float4s per thread
   static_assert(SPL == 1 || SS == 4, "a split thread holds one float4 per slot");
+  static_assert(SPL <= 4, "the y combine covers up to four threads per channel");
   constexpr int TCH = kThreads / SPL;   // channels per workgroup
   constexpr int NB = TCH * NV / kThreads;  // float4s per thread when staging a block
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
@@ -332,11 +334,13 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       if constexpr (!RANK1) bs = 2.f * hb;
       ys[ql] = ffma(hs, Cs[n], ys[ql]);
     }
-    // the channel's y: the balanced tree over its S slices, whose top-level
-    // halves are the two threads' trees when split (fp addition commutes, so
-    // both lanes get the same bits)
+    // the channel's y: the balanced tree over its S slices, whose subtrees of
+    // 4 slices are the threads' trees when split, combined pairwise as the
+    // tree pairs them (fp addition commutes, so every lane of the channel
+    // gets the same bits)
     float ysum = tree_sum<SS>(ys);
-    if constexpr (SPL == 2) ysum = ysum + __shfl_xor(ysum, 1);
+    if constexpr (SPL >= 2) ysum = ysum + __shfl_xor(ysum, 1);
+    if constexpr (SPL >= 4) ysum = ysum + __shfl_xor(ysum, 2);
     if (cvalid && half == 0) {
       float yv = ysum + fmul(uu, dsk);
       if (p.z != nullptr) yv = silu_gate(yv, zz, p.dt_z);
@@ -393,7 +397,7 @@ static hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
 
 template <int S, int NPL>
 static hipError_t launch_step_tile(int gk, const StepParams& p, hipStream_t st) {
-  if constexpr (S * NPL <= 40) {
+  if constexpr (step_tile_shape(S, NPL)) {
     return with_gate_kind<NPL>(gk, [&](auto g) {
       return launch_step_tile_t<S, NPL, decltype(g)>(p, st);
     });

@@ -45,7 +45,8 @@ def to(t):
 
 
 @pytest.mark.parametrize("NR,NT,cplx", [(16, 4, True), (12, 4, True), (8, 0, False), (0, 5, True),
-                                        (32, 8, True), (64, 8, True)])
+                                        (32, 8, True), (64, 8, True), (32, 0, True),
+                                        (40, 8, True), (48, 16, True), (64, 16, False)])
 @pytest.mark.parametrize("fresh", [False, True])
 def test_step_matches_reference_step(gpu_lib, NR, NT, cplx, fresh):
     hip_step = _step()
@@ -84,7 +85,8 @@ def test_step_matches_golden_block_step(gpu_lib):
     assert rel(out, g["out"]) <= 1e-5
 
 
-@pytest.mark.parametrize("NR,NT,L", [(12, 4, 37), (32, 8, 64), (16, 4, 20), (64, 8, 19)])
+@pytest.mark.parametrize("NR,NT,L", [(12, 4, 37), (32, 8, 64), (16, 4, 20), (64, 8, 19),
+                                     (32, 0, 40), (40, 8, 11), (48, 16, 23), (64, 16, 9)])
 def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
     """Stepping token by token reproduces the scan's y and final state bit for bit."""
     from redpanda_amd.scan import hip_scan_with_state
@@ -111,7 +113,7 @@ def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
     assert torch.equal(state[1], b_scan)
 
 
-@pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8)])
+@pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8), (32, 0), (48, 16), (64, 16)])
 def test_step_equals_scan_many_rollouts(gpu_lib, NR, NT):
     """Thousands of rollouts over whole 256-channel tiles (several rollouts
     per workgroup, a short last group): still the scan's bits."""

@@ -118,7 +118,8 @@ def test_step_sweep(gpu_lib, case):
     step and torch's gate, across kernel choices (d_state 4..72)."""
     rng = random.Random(400 + case)
     g = torch.Generator(device=dev).manual_seed(case)
-    NR, NT = rng.choice([(4, 0), (12, 4), (16, 4), (32, 8), (36, 4), (64, 8), (6, 2)])
+    NR, NT = rng.choice([(4, 0), (12, 4), (16, 4), (32, 8), (36, 4), (64, 8), (6, 2), (32, 0),
+                         (48, 16), (40, 8)])
     N, R, D = NR + NT, rng.randint(1, 300), rng.choice([32, 100, 256, 300, 1024])
     x = torch.randn(R, D, device=dev, generator=g) - 2
     u = torch.randn(R, D, device=dev, generator=g)
