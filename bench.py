@@ -63,6 +63,10 @@ SCAN_SHAPE = dict(B=256, L=64, D=1536, NR=32, NT=8)
 # Search-Mamba batched step: 4096 rollouts, 8 causal layers, d_model 512
 # (d_inner 1024 = 16 heads x 64), d_state 16 complex plus 4 tracking.
 STEP_SHAPE = dict(R=4096, layers=8, D=1024, NR=16, NT=4)
+# The step at the reference's default search-model core (SearchMambaConfig,
+# engine/search_mamba.py:28-35: 12 layers, d_model 384 -> d_inner 768,
+# d_state 32, no tracking states), 4096 rollouts.
+STEP_SHAPE_DEFAULT = dict(R=4096, layers=12, D=768, NR=32, NT=0)
 # Long-sequence causal stress: batch 64, L=2048, d_inner 1024, d_state 64
 # complex plus 8 tracking, fp32 inputs.
 LONG_SHAPE = dict(B=64, L=2048, D=1024, NR=64, NT=8)
@@ -276,9 +280,9 @@ def bench_scan(torch, args, dtype):
                 t_inf=t_inf, fwd_bytes=fb, bwd_bytes=bb, T=B * L)
 
 
-def bench_step(torch, args, layers=None, plies=32, keep=True, R=None):
+def bench_step(torch, args, layers=None, plies=32, keep=True, R=None, shape=None):
     from redpanda_amd import _lib
-    sh = STEP_SHAPE
+    sh = STEP_SHAPE if shape is None else shape
     R = sh["R"] if R is None else R
     D, NR, NT = sh["D"], sh["NR"], sh["NT"]
     layers = sh["layers"] if layers is None else layers
@@ -1326,6 +1330,10 @@ def main():
               f"{step['rollout_steps_s_rank1']:.4g} rollout-steps/s, "
               f"{step['t_launch_rank1'] * 1e6:.1f} us/launch, {step['GBps_rank1']:.0f} GB/s",
               file=sys.stderr, flush=True)
+        step_def = bench_step(torch, args, plies=8, shape=STEP_SHAPE_DEFAULT)
+        print(f"[bench] step {STEP_SHAPE_DEFAULT}: {step_def['t_launch'] * 1e6:.1f} us/launch, "
+              f"{step_def['GBps']:.0f} GB/s; rank-1 cache {step_def['t_launch_rank1'] * 1e6:.1f} "
+              f"us/launch, {step_def['GBps_rank1']:.0f} GB/s", file=sys.stderr, flush=True)
     lng = None
     if not args.no_long:
         print(f"[bench] long-sequence scan {LONG_SHAPE} fp32", file=sys.stderr, flush=True)
@@ -1476,6 +1484,20 @@ def main():
                             "(broadcast input state, no copies)",
                 "avg_launch_s": step["t_shared"], "alg_bytes_per_launch": step["bytes_shared"],
                 "achieved_GBps": step["GBps_shared"]},
+            "search_model_default": {
+                "workload": "the step kernel at the reference's default search-model core "
+                            "(SearchMambaConfig: 12 layers, d_inner 768, d_state 32 all "
+                            "rotational), 4096 rollouts, full and rank-1 caches",
+                "config": {**STEP_SHAPE_DEFAULT,
+                           "d_state": STEP_SHAPE_DEFAULT["NR"] + STEP_SHAPE_DEFAULT["NT"]},
+                "rollout_steps_s": STEP_SHAPE_DEFAULT["R"] / (step_def["t_launch"]
+                                                             * STEP_SHAPE_DEFAULT["layers"]),
+                "avg_launch_s": step_def["t_launch"], "alg_bytes_per_launch": step_def["bytes"],
+                "achieved_GBps": step_def["GBps"], "frac": step_def["GBps"] / HBM_PEAK_GBS,
+                "rank1_cache": {"avg_launch_s": step_def["t_launch_rank1"],
+                                "alg_bytes_per_launch": step_def["bytes_rank1"],
+                                "achieved_GBps": step_def["GBps_rank1"],
+                                "frac": step_def["GBps_rank1"] / HBM_PEAK_GBS}},
         }
     if lng is not None:
         trl, vcl = measured_traffic("traffic_long.json"), measured_valu("valu_long.json")

@@ -46,7 +46,8 @@ def to(t):
 
 @pytest.mark.parametrize("NR,NT,cplx", [(16, 4, True), (12, 4, True), (8, 0, False), (0, 5, True),
                                         (32, 8, True), (64, 8, True), (32, 0, True),
-                                        (40, 8, True), (48, 16, True), (64, 16, False)])
+                                        (40, 8, True), (48, 16, True), (64, 16, False),
+                                        (20, 4, True), (72, 8, True)])
 @pytest.mark.parametrize("fresh", [False, True])
 def test_step_matches_reference_step(gpu_lib, NR, NT, cplx, fresh):
     hip_step = _step()
@@ -113,7 +114,8 @@ def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
     assert torch.equal(state[1], b_scan)
 
 
-@pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8), (32, 0), (48, 16), (64, 16)])
+@pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8), (32, 0), (20, 4), (48, 16), (64, 16),
+                                   (72, 8)])
 def test_step_equals_scan_many_rollouts(gpu_lib, NR, NT):
     """Thousands of rollouts over whole 256-channel tiles (several rollouts
     per workgroup, a short last group): still the scan's bits."""
@@ -196,7 +198,8 @@ def test_batched_equals_singles_and_chains(gpu_lib):
             assert torch.equal(si[0][0], chain[0][i])
 
 
-@pytest.mark.parametrize("R,D,NR,NT", [(300, 512, 16, 4), (37, 100, 12, 8), (64, 256, 20, 5)])
+@pytest.mark.parametrize("R,D,NR,NT", [(300, 512, 16, 4), (37, 100, 12, 8), (64, 256, 20, 5),
+                                     (300, 512, 32, 0), (50, 256, 64, 16)])
 def test_broadcast_state_equals_copies(gpu_lib, R, D, NR, NT):
     """A (1, D, N) state expanded to R rollouts (a stride-0 view, read in
     place) steps exactly like its materialised copies."""
