@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // (d_delta, d_u) of one chunk step and channel from its S lanes' partial
   // sums (d gate / d dt, dhb . B) in sDD: the sums over the lanes in the
   // order of reduce_states (pairwise, adjacent halves), then
-  //     d_delta = dga + (dt*u)/2 * sBc,   d_u = dt/2 * sBc
+  //     d_delta = dga + u/2 * sBc,   d_u = dt/2 * sBc   (hb = (dt*u)/2 * B)
   auto dd_of = [&](int buf, int r, int cc, float dt, float uh) -> float2 {
     float2 v[S];
 #pragma unroll
