@@ -2,10 +2,10 @@
 
 At the rollout counts MARS runs (survivors x simulations, a few to a few
 hundred rows: engine/mars_search.py:59, :440-449), one Mamba.step ply is
-bound by the host: each of the n_layer layers issues about ten launches from
-Python (projections, BCNorm, the fused step, the residual add + RMSNorm),
-about 1.5 ms per ply for 8 layers whatever the batch, against 10-60 us of
-step-kernel time.  StepGraph records one ply of Mamba.step for a fixed batch
+bound by the host: each of the n_layer layers issues seven launches from
+Python (four projections, the SiLU, the fused step with BCNorm in its
+prologue, the residual add + RMSNorm), about 1.3 ms per ply for 8 layers up
+to 512 rows, against 8-43 us of step kernel per layer.  StepGraph records one ply of Mamba.step for a fixed batch
 once and replays it: every launch of the ply is issued by one graph launch.
 
 The state lives in two static cache sets that the two captured graphs use in
