@@ -5,8 +5,9 @@ hundred rows: engine/mars_search.py:59, :440-449), one Mamba.step ply is
 bound by the host: each of the n_layer layers issues seven launches from
 Python (four projections, the SiLU, the fused step with BCNorm in its
 prologue, the residual add + RMSNorm), about 1.3 ms per ply for 8 layers up
-to 512 rows, against 8-43 us of step kernel per layer.  StepGraph records one ply of Mamba.step for a fixed batch
-once and replays it: every launch of the ply is issued by one graph launch.
+to 512 rows, against 8-43 us of step kernel per layer.  StepGraph records
+one ply of Mamba.step for a fixed batch once and replays it: every launch of
+the ply is issued by one graph launch.
 
 The state lives in two static cache sets that the two captured graphs use in
 turn (graph 0 reads set 0 and writes set 1, graph 1 the reverse), so a ply
