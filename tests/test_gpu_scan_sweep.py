@@ -18,6 +18,7 @@ that dtype's rounding, norm-wise.
 """
 
 import math
+import os
 import random
 
 import pytest
@@ -32,6 +33,8 @@ FWD_TOL = 1e-5
 GRAD_TOL = 1e-6
 ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
 DTS = [torch.float32, torch.bfloat16, torch.float16]
+# RP_SWEEP_SCALE=k draws k times as many cases (new seeds; the first ones unchanged)
+SCALE = int(os.environ.get("RP_SWEEP_SCALE", "1"))
 
 
 def rel(a, b):
@@ -138,7 +141,7 @@ def _oracle64(delta, u, Bc, Cc, Ar, Ai, Tk, dy, bidir, softplus):
     return y, out
 
 
-@pytest.mark.parametrize("case", range(16))
+@pytest.mark.parametrize("case", range(16 * SCALE))
 def test_scan_shape_sweep(gpu_lib, case):
     from redpanda_amd.scan import hip_trapezoidal_scan
     s = _draw(case)

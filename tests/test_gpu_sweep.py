@@ -4,6 +4,7 @@ strided and offset views, and every storage-dtype combination the C ABI
 accepts.  Each case is small; tolerances as in the per-kernel tests.
 """
 
+import os
 import random
 
 import pytest
@@ -19,10 +20,12 @@ pytestmark = pytest.mark.gpu
 dev = "cuda"
 DTS = [torch.float32, torch.bfloat16, torch.float16]
 ULP = {torch.float32: 2.0 ** -23, torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11}
+# RP_SWEEP_SCALE=k draws k times as many cases (new seeds; the first ones unchanged)
+SCALE = int(os.environ.get("RP_SWEEP_SCALE", "1"))
 
 
 def nrel(a, b):
-    a, b = a.float(), b.float()
+    a, b = a.detach().float(), b.detach().float()
     return float((a - b).abs().max() / (b.abs().max() + 1e-30)) if b.numel() else 0.0
 
 
@@ -33,7 +36,7 @@ def _view(shape, dt, g, pad, scale=1.0):
     return base[..., pad:]
 
 
-@pytest.mark.parametrize("case", range(12))
+@pytest.mark.parametrize("case", range(12 * SCALE))
 def test_mixer_sweep(gpu_lib, case):
     rng = random.Random(100 + case)
     g = torch.Generator(device=dev).manual_seed(case)
@@ -62,7 +65,7 @@ def test_mixer_sweep(gpu_lib, case):
     assert nrel(a[3].grad, r[3].grad) <= tol
 
 
-@pytest.mark.parametrize("case", range(10))
+@pytest.mark.parametrize("case", range(10 * SCALE))
 def test_bcnorm_sweep(gpu_lib, case):
     rng = random.Random(200 + case)
     g = torch.Generator(device=dev).manual_seed(case)
@@ -97,7 +100,7 @@ def test_bcnorm_sweep(gpu_lib, case):
             assert nrel(a[2].grad, r[2].grad) <= 1e-5 and nrel(a[3].grad, r[3].grad) <= 1e-5
 
 
-@pytest.mark.parametrize("case", range(8))
+@pytest.mark.parametrize("case", range(8 * SCALE))
 def test_rmsnorm_sweep(gpu_lib, case):
     rng = random.Random(300 + case)
     g = torch.Generator(device=dev).manual_seed(case)
@@ -112,7 +115,7 @@ def test_rmsnorm_sweep(gpu_lib, case):
     assert torch.equal(xn, xr) and nrel(out, ref) <= 1e-6
 
 
-@pytest.mark.parametrize("case", range(8))
+@pytest.mark.parametrize("case", range(8 * SCALE))
 def test_step_sweep(gpu_lib, case):
     """Gated, softplus-on-load steps in both beta forms against the full-form
     step and torch's gate, across kernel choices (d_state 4..72)."""
@@ -142,7 +145,7 @@ def test_step_sweep(gpu_lib, case):
     assert torch.equal(y1, y0 * F.silu(z))
 
 
-@pytest.mark.parametrize("case", range(8))
+@pytest.mark.parametrize("case", range(8 * SCALE))
 def test_step_bcnorm_sweep(gpu_lib, case):
     """The step from raw B / C projections (BCNorm + p-sum inside the step, or
     the BCNorm kernel first, as the batch decides) equals hip_bcnorm_psum
