@@ -549,8 +549,9 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
   if ((int64_t)p.ntiles * a->R > kI32Max)
     return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   const int gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
-  // the tile kernel moves each channel's (h, beta) as 16-byte vectors
-  const bool tile = a->N % 4 == 0 && S * NPL == a->N && rp::step_tile_shape(S, NPL) &&
+  // the tile kernel moves each channel's (h, beta) as 16-byte vectors (with
+  // pad states when N is below the shape's S * NPL)
+  const bool tile = a->N % 4 == 0 && rp::step_tile_shape(S, NPL) &&
                     aligned(a->h_out, 16) &&
                     (a->h_in == nullptr || aligned(a->h_in, 16)) &&
                     (a->beta_rank1 || (aligned(a->beta_out, 16) &&

@@ -194,7 +194,8 @@ constexpr int kStepTile = kThreads;
 // 8 slices up (d_state 24-40 and 48-80), each thread taking 4 slices (one
 // float4 per slot); the tile then holds kStepTile / (S / 4) channels.
 constexpr int step_tile_split(int S) { return S >= 8 ? S / 4 : 1; }
-// Whether the step tile kernel takes the shape (S, NPL) (d_state = S * NPL).
+// Whether the step tile kernel takes the shape (S, NPL) (d_state a multiple
+// of 4 up to S * NPL).
 constexpr bool step_tile_shape(int S, int NPL) {
   return S * NPL <= 40 || (S == 16 && NPL <= 5);
 }
@@ -225,10 +226,11 @@ hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const Bw
                            hipStream_t st);
 hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc, float* d_Cc,
                                float* d_Ar, float* d_Ai, float* d_Tk, hipStream_t st);
-// `tile`: the tile kernel (N == S*NPL, N % 4 == 0, step_tile_shape, 16-byte
-// aligned state pointers); otherwise the lane-layout kernel.
-// Bitwise the same.
+// `tile`: the tile kernel (N % 4 == 0, step_tile_shape, 16-byte aligned
+// state pointers; N below S*NPL takes its pad-state instantiation,
+// launch_step_tile_pad); otherwise the lane-layout kernel.  Bitwise the same.
 hipError_t launch_step(int S, int NPL, int gk, bool tile, const StepParams& p, hipStream_t st);
+hipError_t launch_step_tile_pad(int S, int NPL, int gk, const StepParams& p, hipStream_t st);
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t st);
 
 // Rollout-ply boundary (ply.hip).

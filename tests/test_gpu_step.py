@@ -47,7 +47,8 @@ def to(t):
 @pytest.mark.parametrize("NR,NT,cplx", [(16, 4, True), (12, 4, True), (8, 0, False), (0, 5, True),
                                         (32, 8, True), (64, 8, True), (32, 0, True),
                                         (40, 8, True), (48, 16, True), (64, 16, False),
-                                        (20, 4, True), (72, 8, True)])
+                                        (20, 4, True), (72, 8, True), (20, 8, True),
+                                        (40, 4, True), (56, 4, False)])
 @pytest.mark.parametrize("fresh", [False, True])
 def test_step_matches_reference_step(gpu_lib, NR, NT, cplx, fresh):
     hip_step = _step()
@@ -87,7 +88,8 @@ def test_step_matches_golden_block_step(gpu_lib):
 
 
 @pytest.mark.parametrize("NR,NT,L", [(12, 4, 37), (32, 8, 64), (16, 4, 20), (64, 8, 19),
-                                     (32, 0, 40), (40, 8, 11), (48, 16, 23), (64, 16, 9)])
+                                     (32, 0, 40), (40, 8, 11), (48, 16, 23), (64, 16, 9),
+                                     (20, 8, 30), (52, 8, 17)])
 def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
     """Stepping token by token reproduces the scan's y and final state bit for bit."""
     from redpanda_amd.scan import hip_scan_with_state
@@ -115,7 +117,7 @@ def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
 
 
 @pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8), (32, 0), (20, 4), (48, 16), (64, 16),
-                                   (72, 8)])
+                                   (72, 8), (20, 8), (36, 8), (52, 8), (64, 8), (68, 8)])
 def test_step_equals_scan_many_rollouts(gpu_lib, NR, NT):
     """Thousands of rollouts over whole 256-channel tiles (several rollouts
     per workgroup, a short last group): still the scan's bits."""
@@ -199,7 +201,8 @@ def test_batched_equals_singles_and_chains(gpu_lib):
 
 
 @pytest.mark.parametrize("R,D,NR,NT", [(300, 512, 16, 4), (37, 100, 12, 8), (64, 256, 20, 5),
-                                     (300, 512, 32, 0), (50, 256, 64, 16)])
+                                     (300, 512, 32, 0), (50, 256, 64, 16), (40, 128, 40, 4),
+                                     (33, 256, 24, 4)])
 def test_broadcast_state_equals_copies(gpu_lib, R, D, NR, NT):
     """A (1, D, N) state expanded to R rollouts (a stride-0 view, read in
     place) steps exactly like its materialised copies."""
@@ -236,6 +239,9 @@ def test_in_place_state_update(gpu_lib):
     (700, 1024, 16, 4, 2, True, torch.float32, "full"),     # several rollouts per workgroup
     (700, 1024, 16, 4, 2, True, torch.bfloat16, "rank1"),
     (6, 96, 12, 6, 2, True, torch.float32, "full"),         # d_state 18: the lane kernel
+    (4, 256, 20, 8, 2, True, torch.float32, "rank1"),       # d_state 28: pad states, fused
+    (3, 192, 52, 8, 2, True, torch.bfloat16, "shared"),     # d_state 60: pad states, fused
+    (600, 512, 36, 8, 2, True, torch.float32, "full"),      # d_state 44: pad states, BCNorm first
 ])
 def test_step_bcnorm_equals_bcnorm_then_step(gpu_lib, R, D, NR, NT, P, norm, dt, form):
     """rp_step_bcnorm (BCNorm + p-sum of the raw x_proj projections inside the
