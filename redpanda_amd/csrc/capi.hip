@@ -66,8 +66,19 @@ int step_ri_override() {
   return v;
 }
 
+// Tiles per backward workgroup forced by RP_BWD_TPW (1-8, for measurements);
+// 0: the plan's own choice.
+int bwd_tpw_override() {
+  static int v = [] {
+    const char* s = getenv("RP_BWD_TPW");
+    const int x = s ? atoi(s) : 0;
+    return (x >= 1 && x <= 8) ? x : 0;
+  }();
+  return v;
+}
+
 struct Plan {
-  int S, NPL, CB, ntiles, nck, ndir, bg, nbg;
+  int S, NPL, CB, ntiles, nck, ndir, bg, nbg, tpw, ntg;
   int gk;     // gate kind: rotational / tracking split fixed at compile time
   int64_t ckpt_bytes, part_bc_bytes, part_par_bytes;
   int64_t dcache_off;  // byte offset of the softplus(x) cache in the workspace, or -1
@@ -147,6 +158,22 @@ Plan make_plan(const rp_scan_args* a) {
   if (bg > 8) bg = 8;
   pl.bg = (int)bg;
   pl.nbg = (int)((a->B + bg - 1) / bg);
+  // adjacent channel tiles per backward workgroup: where a tile is 16
+  // channels (16 lanes per channel), a workgroup walks 4 (or 2) tiles in
+  // turn and their dB / dC partials add up in one block, so the partials
+  // and the reduction's reads shrink by that factor, as long as the grid
+  // keeps at least 1024 workgroups
+  pl.tpw = 1;
+  if (S == 16) {
+    for (int t : {4, 2}) {
+      if (pl.ntiles % t == 0 && (int64_t)(pl.ntiles / t) * pl.nbg >= 1024) {
+        pl.tpw = t;
+        break;
+      }
+    }
+  }
+  if (bwd_tpw_override() > 0 && S == 16) pl.tpw = bwd_tpw_override();
+  pl.ntg = (pl.ntiles + pl.tpw - 1) / pl.tpw;
   pl.ckpt_bytes = (int64_t)pl.ndir * a->B * pl.nck * pl.ntiles * rp::kThreads * NPL * 4;
   // with softplus the forward also keeps delta = softplus(x) for the
   // backward, which then stages it as stored
@@ -155,7 +182,7 @@ Plan make_plan(const rp_scan_args* a) {
     pl.dcache_off = round_up(pl.ckpt_bytes, 256);
     pl.ckpt_bytes = pl.dcache_off + a->B * a->L * a->D * 4;
   }
-  pl.part_bc_bytes = round_up(2 * (int64_t)pl.ntiles * a->B * a->L * a->N * 4, 256);
+  pl.part_bc_bytes = round_up(2 * (int64_t)pl.ntg * a->B * a->L * a->N * 4, 256);
   pl.part_par_bytes = round_up((int64_t)pl.nbg * 2 * a->D * a->N * 8, 256);
   return pl;
 }
@@ -387,7 +414,7 @@ int scan_bwd_impl(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream,
     if (st != RP_OK) return st;
   }
   if (a->D == 0) return RP_OK;
-  if ((int64_t)pl.ntiles * pl.nbg > kI32Max)
+  if ((int64_t)pl.ntg * pl.nbg > kI32Max)
     return fail(RP_ERR_UNSUPPORTED, "scan bwd: grid too large");
   const rp::ScanParams p = scan_params(a, pl);
   rp::BwdIO b{};
@@ -407,6 +434,8 @@ int scan_bwd_impl(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream,
   b.part_par = reinterpret_cast<double*>(static_cast<char*>(scr) + pl.part_bc_bytes);
   b.bg = pl.bg;
   b.nbg = pl.nbg;
+  b.tpw = pl.tpw;
+  b.ntg = pl.ntg;
   hipStream_t s = (hipStream_t)stream;
   if (a->B > 0) {
     hipError_t e = rp::launch_scan_bwd(pl.S, pl.NPL, pl.gk, p, b, s);

@@ -52,10 +52,12 @@ struct BwdIO {
   float* d_h0;       // (B, D, N) or null
   float* d_beta0;
   const float* dcache;  // (B, L, D) delta = softplus(x) cached by the forward (dsp only)
-  float* part_bc;    // [2][ntiles][B][L][N]  per-tile dB / dC partial sums
+  float* part_bc;    // [2][ntg][B][L][N]     per-tile-group dB / dC partial sums
   double* part_par;  // [nbg][2][D][N]        per-batch-group dA partial sums
   int bg;           // batch rows per workgroup
   int nbg;          // ceil(B / bg)
+  int tpw;          // adjacent channel tiles per workgroup (a tile group)
+  int ntg;          // ceil(ntiles / tpw)
 };
 
 struct StepParams {

@@ -7,7 +7,7 @@
 
 namespace rp {
 
-// dB / dC: sum the per-tile partials in a fixed order (fp64 accumulator).
+// dB / dC: sum the per-tile-group partials in a fixed order (fp64 accumulator).
 // The loads do not depend on the sum, so the unrolled loop keeps 8 of them in
 // flight while the additions stay in tile order.  bwd_reduce_bc4 sums four
 // adjacent elements per thread with 16-byte loads (the same additions in the
@@ -91,8 +91,16 @@ static bool bwd_fast(const ScanParams& p, const BwdIO& io, int CB) {
 
 template <int S, int NPL, class GK>
 static hipError_t launch_bwd_t(const ScanParams& p, const BwdIO& io, hipStream_t st) {
-  dim3 grid((unsigned)((int64_t)p.ntiles * io.nbg));
-  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, false>), grid, dim3(kThreads), 0, st, p, io);
+  dim3 grid((unsigned)((int64_t)io.ntg * io.nbg));
+  if constexpr (S == 16) {
+    if (io.tpw > 1) {
+      hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, false, true>), grid, dim3(kThreads), 0, st,
+                         p, io);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, false, false>), grid, dim3(kThreads), 0, st, p,
+                     io);
   return hipGetLastError();
 }
 
@@ -116,13 +124,13 @@ hipError_t launch_bwd_finalize(const ScanParams& p, const BwdIO& io, float* d_Bc
   if (per > 0 && per % 4 == 0 && al16(io.part_bc) && al16(d_Bc) && al16(d_Cc)) {
     const int64_t n = 2 * (per / 4);
     hipLaunchKernelGGL(bwd_reduce_bc4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       (const float4*)io.part_bc, (float4*)d_Bc, (float4*)d_Cc, per / 4, p.ntiles);
+                       (const float4*)io.part_bc, (float4*)d_Bc, (float4*)d_Cc, per / 4, io.ntg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   } else if (per > 0) {
     const int64_t n = 2 * per;
     hipLaunchKernelGGL(bwd_reduce_bc, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       (const float*)io.part_bc, d_Bc, d_Cc, per, p.ntiles);
+                       (const float*)io.part_bc, d_Bc, d_Cc, per, io.ntg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -8,8 +8,16 @@ namespace rp {
 
 template <int S, int NPL, class GK>
 static hipError_t launch_bwd_fast_t(const ScanParams& p, const BwdIO& io, hipStream_t st) {
-  dim3 grid((unsigned)((int64_t)p.ntiles * io.nbg));
-  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, true>), grid, dim3(kThreads), 0, st, p, io);
+  dim3 grid((unsigned)((int64_t)io.ntg * io.nbg));
+  if constexpr (S == 16) {
+    if (io.tpw > 1) {
+      hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, true, true>), grid, dim3(kThreads), 0, st,
+                         p, io);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, true, false>), grid, dim3(kThreads), 0, st, p,
+                     io);
   return hipGetLastError();
 }
 

@@ -71,8 +71,14 @@ constexpr int kParChunks = 16;
 // full-rate add per staged element, where the general form multiplies 64-bit
 // indices per element and chunk.  Both instantiations compute the same
 // values in the same order.
-template <int S, int NPL, class GK, bool FAST>
-__global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
+// One channel tile's backward over the workgroup's batch rows: tile `tile`,
+// the tpass-th of the io.tpw adjacent tiles the workgroup walks (tile group
+// tgrp), batch group bgi.  The tiles of a group share one dB / dC partial
+// block: the first writes it, the others add onto it (as the reverse
+// direction adds onto the forward direction's), in tile order.
+template <int S, int NPL, class GK, bool FAST, bool MULTI>
+__device__ __forceinline__ void scan_bwd_tile(const ScanParams& p, const BwdIO& io, int tile,
+                                              int tpass, int tgrp, int bgi) {
   using Sh = Shape<S, NPL>;
   // ALT: the entry state is prefetched into two buffers that alternate with
   // the LDS slot (the chunk in slot SL enters from buffer SL and loads the
@@ -140,12 +146,15 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // global partials when PAR_GLOBAL)
   __shared__ double sPar[PAR_GLOBAL ? 1 : 2][PAR_GLOBAL ? 1 : NPL][PAR_GLOBAL ? 1 : kThreads];
 
-  const int tid = threadIdx.x;
+  // MULTI (a walk over several tiles): the thread index through an opaque
+  // copy, so that what derives from it is computed per tile instead of
+  // hoisted out of the walk and held in registers across it
+  int tid = threadIdx.x;
+  if constexpr (MULTI) asm volatile("" : "+v"(tid));
   const int wave = tid / kWave, lane = tid % kWave;
   const int dl = lane / S, s = lane % S;
   const int cl = wave * DT + dl;
   const int wrow = wave * 4 + lane / 16;  // row index within the workgroup
-  const int tile = blockIdx.x % p.ntiles, bgi = blockIdx.x / p.ntiles;
   const int c = tile * CB + cl;
   const bool cvalid = FAST || c < p.D;
   const bool has_imag = p.Ai != nullptr;
@@ -153,7 +162,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 
   GateRegs<NPL> gp;  // loads issued first, so the table copy overlaps them
   load_gate_regs<S, NPL>(gp, p.Ar, p.Ai, p.Tk, c, s, p.N, p.NR, p.NT, cvalid);
-  fill_sincos_pairs(sCS, tid);  // first read after the staging barrier below
+  // first read after the staging barrier below (the table stays from the
+  // workgroup's first tile on)
+  if (tpass == 0) fill_sincos_pairs(sCS, tid);
   // pam: the coefficient of the ddt sum over rotational states, zero for a
   // tracking state (only read for slots whose kind is decided at run time)
   float pam[NPL];
@@ -192,7 +203,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
   // at chunk 0, and the wave-uniform byte step per chunk: the offset at chunk
   // ch is o + ch * step (mod 2^32; the elements a lane loads or stores lie in
   // their arrays, whose spans fit in 32 bits).  oF is relative to the
-  // sweep's (tile, b) block of the dB / dC partials, pbc.
+  // sweep's (tile group, b) block of the dB / dC partials, pbc.
   uint32_t oDT[CPT], oU[CPT], oDY[CPT], oB[SPT], oC[SPT], oF[NFOLD][FPT], oD[DPT];
   uint32_t stDT = 0, stU = 0, stDY = 0, stB = 0, stC = 0, stF = 0;
   float* pbc = io.part_bc;
@@ -240,7 +251,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       oB[k] = (uint32_t)((b * p.bsb + t * p.bsl + n) * es_b);
       oC[k] = (uint32_t)((b * p.csb + t * p.csl + n) * es_c);
     }
-    const int64_t half = (int64_t)p.ntiles * p.B * L * p.N;  // the dC half of the partials
+    const int64_t half = (int64_t)io.ntg * p.B * L * p.N;  // the dC half of the partials
 #pragma unroll
     for (int f = 0; f < NFOLD; ++f) {
 #pragma unroll
@@ -263,7 +274,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     stB = (uint32_t)(sg * K * p.bsl * es_b);
     stC = (uint32_t)(sg * K * p.csl * es_c);
     stF = (uint32_t)(sg * K * p.N * 4);
-    pbc = io.part_bc + ((int64_t)tile * p.B + b) * L * p.N;
+    pbc = io.part_bc + ((int64_t)tgrp * p.B + b) * L * p.N;
   };
   // FAST: the storage codes of (delta as staged, u, B and C) as one of the
   // common combinations, fixed at compile time in the staging code, so that
@@ -445,7 +456,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       for (int j = 0; j < NPL; ++j) dst[j] = src[j * kWave];
     }
   };
-  // The (which, t, n) partial of tile `tile`, batch row b that fold output e
+  // The (which, t, n) partial of tile group tgrp, batch row b that fold output e
   // of the fold starting at chunk step mf writes; null when beyond the chunk.
   auto fold_dst = [&](int e, int b, int dir, int i0, int mf, int kcnt) -> float* {
     const int rr = e / (2 * p.N);
@@ -453,7 +464,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
     const int rem = e % (2 * p.N);
     const int which = rem / p.N, n = rem % p.N;
     const int t = tix(dir, i0 + mf + rr);
-    return io.part_bc + (((int64_t)which * p.ntiles + tile) * p.B + b) * ((int64_t)L * p.N) +
+    return io.part_bc + (((int64_t)which * io.ntg + tgrp) * p.B + b) * ((int64_t)L * p.N) +
            (int64_t)t * p.N + n;
   };
   // The d_delta / d_u element of chunk step e / CB, channel e % CB; -1 when
@@ -496,6 +507,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
       // to its dhb (gr, used at that step only: fin).
       float qn[NPL], gn[NPL], gr[NPL];
       bool fin = false;
+      // dB / dC partials added onto the block's values: the reverse
+      // direction, and every sweep of the group's later tiles
+      const bool add_bc = dir == 1 || tpass > 0;
       if constexpr (FAST) fast_sweep(b, dir);
 #pragma unroll
       for (int j = 0; j < NPL; ++j) {
@@ -556,8 +570,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
         float prev[NFOLD][FPT], pdd[DPT][2];
         float hc[NPL], hbp[NPL];
         // loads a chunk ahead: the inputs of chunk ch-1, the partials the
-        // reverse direction adds to (dB / dC and d_delta / d_u), and the
-        // state entering chunk ch-1 (into `next`)
+        // reverse direction adds to (dB / dC and d_delta / d_u; dB / dC also
+        // from the tile group's second tile on), and the state entering
+        // chunk ch-1 (into `next`)
         auto issue_loads = [&](float (&next)[NPL]) {
           if (ch >= 1) stage_load(b, dir, ch - 1);
 #pragma unroll
@@ -566,9 +581,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
             for (int k = 0; k < FPT; ++k) {
               prev[f][k] = 0.f;
               if constexpr (FAST) {
-                if (dir == 1 && fInfo[k] >= 0 && f * KR + (fInfo[k] & 7) < kcnt)
+                if (add_bc && fInfo[k] >= 0 && f * KR + (fInfo[k] & 7) < kcnt)
                   prev[f][k] = load_byte<float>(pbc, oF[f][k] + (uint32_t)ch * stF);
-              } else if (dir == 1) {
+              } else if (add_bc) {
                 const float* src = fold_dst(tid + k * kThreads, b, dir, i0, f * KR, kcnt);
                 if (src != nullptr) prev[f][k] = *src;
               }
@@ -781,7 +796,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                     const float v = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
                                     (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
                     store_byte<float>(pbc, oF[m / KR][k] + (uint32_t)ch * stF,
-                                      dir == 0 ? v : prev[m / KR][k] + v);
+                                      add_bc ? prev[m / KR][k] + v : v);
                   }
                   continue;
                 }
@@ -795,7 +810,7 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
                   const float4 a0 = rp[0], a1 = rp[1], a2 = rp[2], a3 = rp[3];
                   const float v = (((a0.x + a0.y) + (a0.z + a0.w)) + ((a1.x + a1.y) + (a1.z + a1.w))) +
                                   (((a2.x + a2.y) + (a2.z + a2.w)) + ((a3.x + a3.y) + (a3.z + a3.w)));
-                  *dst = dir == 0 ? v : prev[m / KR][k] + v;
+                  *dst = add_bc ? prev[m / KR][k] + v : v;
                 }
               }
               if (m == 0) {
@@ -922,6 +937,25 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
         }
       }
     }
+  }
+}
+
+// The backward kernel: workgroup = tile group x batch group.  MULTI: it
+// walks the group's io.tpw adjacent channel tiles in turn (fewer dB / dC
+// partials to write and reduce where tiles are narrow: 16 channels at 16
+// lanes); otherwise one tile (io.tpw == 1), without the loop, whose
+// hoisting would cost registers.
+template <int S, int NPL, class GK, bool FAST, bool MULTI>
+__global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(ScanParams p, BwdIO io) {
+  const int tgrp = blockIdx.x % io.ntg, bgi = blockIdx.x / io.ntg;
+  if constexpr (MULTI) {
+    for (int tp = 0; tp < io.tpw; ++tp) {
+      const int tile = tgrp * io.tpw + tp;
+      if (tile >= p.ntiles) break;
+      scan_bwd_tile<S, NPL, GK, FAST, true>(p, io, tile, tp, tgrp, bgi);
+    }
+  } else {
+    scan_bwd_tile<S, NPL, GK, FAST, false>(p, io, tgrp, 0, tgrp, bgi);
   }
 }
 
