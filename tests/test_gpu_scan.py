@@ -283,6 +283,31 @@ def test_whole_tile_backward_equals_general(gpu_lib, NR, NT, D, softplus):
             assert torch.equal(g1[k], g3[k]), f"initial state, {k}"
 
 
+@pytest.mark.parametrize("D", [128, 120])
+@pytest.mark.parametrize("bidir", [False, True])
+def test_backward_tile_walk_matches_single_tile(gpu_lib, D, bidir):
+    """At 16 lanes per channel (16-channel tiles) a large batch has each
+    backward workgroup walk 4 adjacent channel tiles, whose dB / dC partials
+    add into one block; a single batch row runs one tile per workgroup.  Rows
+    are independent, so every checked row of the large batch has the
+    single-row run's bits in y, d_delta and d_u (per-channel sums), and its
+    dB / dC within about one fp32 rounding per tile (their partials are added
+    in another order).  D=120 leaves a partial tile: the general
+    instantiation walks too."""
+    B, L, NR, NT = 1100, 9, 64, 8
+    c = make_case(808, B=B, L=L, D=D, NR=NR, NT=NT)
+    y, g = hip_capi.scan_fwd_bwd(c, bidir)
+    for r in (0, 517, B - 1):
+        cr = {k: (v[r:r + 1] if k in ("delta", "u", "Bc", "Cc", "dy") else v) for k, v in c.items()}
+        yr, gr = hip_capi.scan_fwd_bwd(cr, bidir)
+        assert torch.equal(y[r:r + 1], yr), r
+        assert torch.equal(g["delta"][r:r + 1], gr["delta"]), r
+        assert torch.equal(g["u"][r:r + 1], gr["u"]), r
+        for k in ("Bc", "Cc"):
+            e = rel(g[k][r:r + 1], gr[k])
+            assert e <= 1e-6, f"row {r} d{k}: {e:.2e}"
+
+
 def test_linearity_in_u(gpu_lib):
     scan, _ = _scan()
     c = make_case(501, B=2, L=40, D=64, NR=12, NT=4)
