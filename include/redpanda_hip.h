@@ -390,7 +390,7 @@ int rp_scan_bwd(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream);
 
 /*
  * rp_scan_bwd without a caller workspace: the same kernels, with their
- * scratch (the per-tile dB / dC partials and the per-batch-group parameter
+ * scratch (the dB / dC partials per tile group and the per-batch-group parameter
  * gradient partials) in a static device array of RP_SCAN_BWD_SCRATCH_BYTES
  * that the library holds on every GPU it runs on until the process ends.
  * No counterpart in the reference: it is for callers that cannot allocate
