@@ -581,6 +581,7 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
   // the tile kernel moves each channel's (h, beta) as 16-byte vectors (with
   // pad states when N is below the shape's S * NPL)
   const bool tile = a->N % 4 == 0 && rp::step_tile_shape(S, NPL) &&
+                    (a->N == S * NPL || a->N > S * (NPL - 1)) &&
                     aligned(a->h_out, 16) &&
                     (a->h_in == nullptr || aligned(a->h_in, 16)) &&
                     (a->beta_rank1 || (aligned(a->beta_out, 16) &&
@@ -604,7 +605,8 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
       if (ri < 1) ri = 1;
       if (ri > ri_max) ri = ri_max;
     }
-    if (ri > rp::kStepRiMax) return fail(RP_ERR_UNSUPPORTED, "step: rollouts per workgroup");
+    if (ri > rp::step_tile_ri_max(S, NPL, a->beta_rank1 != 0))
+      return fail(RP_ERR_UNSUPPORTED, "step: rollouts per workgroup");
     p.ri = (int)ri;
     p.rgroups = (int)((a->R + ri - 1) / ri);
     if ((int64_t)p.ctiles * p.rgroups > kI32Max)

@@ -197,11 +197,18 @@ constexpr int kStepTile = kThreads;
 // float4 per slot); the tile then holds kStepTile / (S / 4) channels.
 constexpr int step_tile_split(int S) { return S >= 8 ? S / 4 : 1; }
 // Whether the step tile kernel takes the shape (S, NPL) (d_state a multiple
-// of 4 up to S * NPL).
+// of 4 up to S * NPL, above S * (NPL - 1) when below S * NPL: pad states
+// only in the last slot).
 constexpr bool step_tile_shape(int S, int NPL) {
-  return S * NPL <= 40 || (S == 16 && NPL <= 5);
+  return S * NPL <= 40 || S == 16;
 }
 constexpr int kStepRiMax = 16;
+// The most rollouts a step tile workgroup walks: above 80 states the B / C
+// rows of fewer rollouts stay in LDS, so that two workgroups fit a CU beside
+// the (h, beta) blocks (the host's automatic choice never exceeds these).
+constexpr int step_tile_ri_max(int S, int NPL, bool rank1) {
+  return S * NPL > 80 ? (rank1 ? 8 : 4) : kStepRiMax;
+}
 
 // Chosen lane split for a state dimension N: S lanes per channel holding NPL
 // states each.  Returns false when N is beyond the compiled shapes.

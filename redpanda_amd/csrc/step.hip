@@ -8,9 +8,10 @@
 //
 // Two kernels, bitwise the same as each other and as the scan:
 //   * step_tile_kernel (step_tile.h; the rollout path: d_state a multiple of
-//     4 up to 80; step_pad.hip instantiates it for d_state below the lane
-//     shape's S*NPL, e.g. 28, 36, 44-60, 68-76): a workgroup owns 256 / SPL
-//     channels and walks a few rollouts.  Per rollout, the (channels x d_state) blocks of
+//     4 up to 128, with pad states only in the last slot; step_pad.hip
+//     instantiates it for d_state below the lane shape's S*NPL, e.g. 28,
+//     36, 44-60, 68-76, 84-92, 116-124): a workgroup owns 256 / SPL channels
+//     and walks a few rollouts.  Per rollout, the (channels x d_state) blocks of
 //     h and beta move with coalesced streaming 16-byte loads and stores
 //     through LDS, where SPL threads per channel (1 up to d_state 20, then
 //     one per 4 slices) update its states; the gate parameters stay in

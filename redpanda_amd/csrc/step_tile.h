@@ -64,7 +64,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   static_assert(FULLD || !SHARED, "the shared-state instantiation is for whole tiles");
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
-  // SPL threads per channel: from 8 slices up (d_state 24-40, 48-80) a
+  // SPL threads per channel: from 8 slices up (d_state 24-40, 44-128) a
   // channel's states split between S / 4 adjacent lanes, 4 slices each (one
   // float4 per slot), so that the gate parameters and the states of a thread
   // fit the registers of several waves per SIMD (one thread per channel took
@@ -79,8 +79,9 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int TCH = kThreads / SPL;   // channels per workgroup
   constexpr int NB = TCH * NV / kThreads;  // float4s per thread when staging a block (at most)
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
+  constexpr int RIM = step_tile_ri_max(S, NPL, RANK1);  // rollouts per workgroup, at most
   __shared__ float2 sCos[kTab];           // (m, b (-sin a)) records of the gate table
-  __shared__ float sBC[kStepRiMax][NBC * NP];  // B, C (B_prev) rows of the workgroup's rollouts
+  __shared__ float sBC[RIM][NBC * NP];    // B, C (B_prev) rows of the workgroup's rollouts
   // the (h, beta) block of one rollout: TCH channels x N states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NVM
   __shared__ float4 sH[TCH * NV], sBt[TCH * NV];
@@ -101,11 +102,11 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   const int nvalid = (FULLD && !PAD) ? TCH * NV : (FULLD ? TCH : min(TCH, p.D - c0)) * NVM;
   const bool has_imag = p.Ai != nullptr;
   const int r_lo = rg * p.ri;
-  const int nr = min(p.R, r_lo + p.ri) - r_lo;  // <= kStepRiMax (checked by the host)
+  const int nr = min(p.R, r_lo + p.ri) - r_lo;  // <= RIM (checked by the host)
   // The prologue issues every load (B / C rows, gate parameters, D) before
   // it stores anything, so their latencies overlap.  The B / C rows of all
   // the workgroup's rollouts are staged once, pad states as zeros.
-  constexpr int BCPT = (kStepRiMax * NBC * NP + kThreads - 1) / kThreads;
+  constexpr int BCPT = (RIM * NBC * NP + kThreads - 1) / kThreads;
   float bc[BCPT];
 #pragma unroll
   for (int k = 0; k < BCPT; ++k) {

@@ -44,12 +44,14 @@ def _rank1_state(R, D, N, seed):
     return h, bp, full_beta(bp, D).contiguous()
 
 
-# (R, D, NR, NT): tile kernel (d_state % 4 == 0 up to 80; from d_state 24
-# each channel split over S / 4 threads; pad states at d_state 28, 44, 72),
-# partial channel tiles, and the lane-layout kernel (d_state 6, 90)
+# (R, D, NR, NT): tile kernel (d_state % 4 == 0 up to 128; from d_state 24
+# each channel split over S / 4 threads; pad states at d_state 28, 44, 72,
+# 116), partial channel tiles, and the lane-layout kernel (d_state 6, 90,
+# and 108, whose pads would span two slots)
 SHAPES = [(300, 1024, 16, 4), (37, 200, 32, 8), (9, 96, 64, 8), (11, 130, 4, 2),
           (65, 384, 48, 16), (7, 100, 24, 8), (20, 192, 72, 8), (33, 256, 20, 8),
-          (70, 512, 36, 8), (5, 64, 80, 10)]
+          (70, 512, 36, 8), (5, 64, 80, 10), (40, 256, 112, 16), (9, 70, 100, 16),
+          (6, 128, 100, 8)]
 
 
 @pytest.mark.parametrize("R,D,NR,NT", SHAPES)

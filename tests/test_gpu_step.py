@@ -48,7 +48,8 @@ def to(t):
                                         (32, 8, True), (64, 8, True), (32, 0, True),
                                         (40, 8, True), (48, 16, True), (64, 16, False),
                                         (20, 4, True), (72, 8, True), (20, 8, True),
-                                        (40, 4, True), (56, 4, False)])
+                                        (40, 4, True), (56, 4, False), (80, 16, True),
+                                        (120, 8, True), (100, 16, True)])
 @pytest.mark.parametrize("fresh", [False, True])
 def test_step_matches_reference_step(gpu_lib, NR, NT, cplx, fresh):
     hip_step = _step()
@@ -117,7 +118,8 @@ def test_step_equals_scan_bitwise(gpu_lib, NR, NT, L):
 
 
 @pytest.mark.parametrize("NR,NT", [(16, 4), (12, 8), (28, 8), (32, 0), (20, 4), (48, 16), (64, 16),
-                                   (72, 8), (20, 8), (36, 8), (52, 8), (64, 8), (68, 8)])
+                                   (72, 8), (20, 8), (36, 8), (52, 8), (64, 8), (68, 8),
+                                   (76, 8), (80, 16), (100, 16), (112, 16), (128, 0), (90, 14)])
 def test_step_equals_scan_many_rollouts(gpu_lib, NR, NT):
     """Thousands of rollouts over whole 256-channel tiles (several rollouts
     per workgroup, a short last group): still the scan's bits."""
