@@ -49,6 +49,7 @@ def _torch_lib_dir():
 FILE_FLAGS = {
     "scan_bwd.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "scan_bwd_fast.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
+    "scan_bwd_walk.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
 }
 
 

@@ -92,13 +92,6 @@ static bool bwd_fast(const ScanParams& p, const BwdIO& io, int CB) {
 template <int S, int NPL, class GK>
 static hipError_t launch_bwd_t(const ScanParams& p, const BwdIO& io, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)io.ntg * io.nbg));
-  if constexpr (S == 16) {
-    if (io.tpw > 1) {
-      hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, false, true>), grid, dim3(kThreads), 0, st,
-                         p, io);
-      return hipGetLastError();
-    }
-  }
   hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, false, false>), grid, dim3(kThreads), 0, st, p,
                      io);
   return hipGetLastError();
@@ -107,6 +100,7 @@ static hipError_t launch_bwd_t(const ScanParams& p, const BwdIO& io, hipStream_t
 hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const BwdIO& io,
                            hipStream_t st) {
   if (S > 0 && bwd_fast(p, io, kWaves * (kWave / S))) return launch_scan_bwd_fast(S, NPL, gk, p, io, st);
+  if (io.tpw > 1) return launch_scan_bwd_walk(S, NPL, gk, false, p, io, st);
 #define RP_CASE(SS, NN)                                                              \
   if (S == SS && NN == NPL)                                                          \
     return with_gate_kind<NN>(gk, [&](auto g) {                                      \

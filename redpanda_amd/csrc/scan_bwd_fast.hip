@@ -9,13 +9,6 @@ namespace rp {
 template <int S, int NPL, class GK>
 static hipError_t launch_bwd_fast_t(const ScanParams& p, const BwdIO& io, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)io.ntg * io.nbg));
-  if constexpr (S == 16) {
-    if (io.tpw > 1) {
-      hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, true, true>), grid, dim3(kThreads), 0, st,
-                         p, io);
-      return hipGetLastError();
-    }
-  }
   hipLaunchKernelGGL((scan_bwd_kernel<S, NPL, GK, true, false>), grid, dim3(kThreads), 0, st, p,
                      io);
   return hipGetLastError();
@@ -23,6 +16,7 @@ static hipError_t launch_bwd_fast_t(const ScanParams& p, const BwdIO& io, hipStr
 
 hipError_t launch_scan_bwd_fast(int S, int NPL, int gk, const ScanParams& p, const BwdIO& io,
                                 hipStream_t st) {
+  if (io.tpw > 1) return launch_scan_bwd_walk(S, NPL, gk, true, p, io, st);
 #define RP_CASE(SS, NN)                                                              \
   if (S == SS && NN == NPL)                                                          \
     return with_gate_kind<NN>(gk, [&](auto g) {                                      \

@@ -962,5 +962,9 @@ __global__ __launch_bounds__(kThreads, NPL <= 5 ? 2 : 1) void scan_bwd_kernel(Sc
 // The whole-tile (FAST) launches, instantiated in scan_bwd_fast.hip.
 hipError_t launch_scan_bwd_fast(int S, int NPL, int gk, const ScanParams& p, const BwdIO& io,
                                 hipStream_t st);
+// The tile-walking (MULTI) launches of the 16-lane shapes, whole-tile or
+// general, instantiated in scan_bwd_walk.hip.
+hipError_t launch_scan_bwd_walk(int S, int NPL, int gk, bool fast, const ScanParams& p,
+                                const BwdIO& io, hipStream_t st);
 
 }  // namespace rp
