@@ -612,6 +612,12 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
     if ((int64_t)p.ctiles * p.rgroups > kI32Max)
       return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   }
+  // the tile kernel's all-rotational gate kind: no slot's split decided at
+  // run time (the default configurations: d_state 32 and 64, no tracking)
+  const int gk_launch = (tile && a->A_imag != nullptr && a->NR == (int64_t)S * NPL &&
+                         a->N == a->NR)
+                            ? rp::kGateRotAll
+                            : gk;
   // (the prologue's BCNorm takes a state per lane: d_state <= 64)
   if (bn != nullptr && tile && p.ri == 1 && a->N <= rp::kWave) {
     p.bn_fused = 1;
@@ -629,7 +635,7 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
     st = rp_bcnorm_fwd(bn, stream);
     if (st != RP_OK) return st;
   }
-  hipError_t e = rp::launch_step(S, NPL, gk, tile, p, (hipStream_t)stream);
+  hipError_t e = rp::launch_step(S, NPL, gk_launch, tile, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "step launch");
   return RP_OK;
 }

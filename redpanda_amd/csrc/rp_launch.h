@@ -222,6 +222,8 @@ enum GateCode {
   kGateRotLead = 1,   // complex gates, slots j < NPL-1 rotational (NR >= S*(NPL-1))
   kGateRotTrack = 2,  // complex gates, slots j < NPL-1 rotational, slot NPL-1
                       // tracking or padding (NR == S*(NPL-1))
+  kGateRotAll = 3,    // step tile kernel only: complex gates, every slot
+                      // rotational (NR == N == S*NPL)
 };
 
 inline int gate_code(bool has_imag, int64_t NR, int S, int NPL) {
