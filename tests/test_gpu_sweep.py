@@ -145,6 +145,39 @@ def test_step_sweep(gpu_lib, case):
     assert torch.equal(y1, y0 * F.silu(z))
 
 
+@pytest.mark.parametrize("case", range(16 * SCALE))
+def test_step_scan_sweep(gpu_lib, case):
+    """One step from a cached state against a length-1 scan from the same
+    state, bit for bit (y, h, beta), over d_state 1..128 with random
+    rotational / tracking splits, rollout and channel counts: every step
+    kernel choice (lane layout; tile with 1, 2 or 4 threads per channel, pad
+    states, each gate kind)."""
+    from redpanda_amd.scan import hip_scan_with_state
+    rng = random.Random(900 + case)
+    g = torch.Generator(device=dev).manual_seed(900 + case)
+    N = rng.choice([rng.randint(1, 128), 4 * rng.randint(1, 32)])
+    NR = rng.choice([N, 0, rng.randint(0, N)])
+    NT = N - NR
+    cplx = NR > 0 and rng.random() < 0.85
+    R, D = rng.randint(1, 600), rng.choice([16, 64, 100, 256, 512])
+    dt = F.softplus(torch.randn(R, D, device=dev, generator=g) * 0.5 - 2.0)
+    u = torch.randn(R, D, device=dev, generator=g)
+    Bc = torch.randn(R, N, device=dev, generator=g)
+    Cc = torch.randn(R, N, device=dev, generator=g)
+    Ar = -torch.exp(torch.rand(D, NR, device=dev, generator=g) * 3) if NR else None
+    Ai = (torch.rand(D, NR, device=dev, generator=g) * 2 - 1) * 3 if cplx else None
+    Tk = torch.tanh(torch.randn(D, NT, device=dev, generator=g)) if NT else None
+    h = torch.randn(R, D, N, device=dev, generator=g)
+    b = torch.randn(R, D, N, device=dev, generator=g) * 0.3
+    print(f"[step scan sweep {case}] R={R} D={D} N={N} NR={NR} NT={NT} complex={cplx}", flush=True)
+    with torch.no_grad():
+        y_s, (h_s, b_s) = hip_scan_with_state(dt[:, None], u[:, None], Bc[:, None], Cc[:, None],
+                                              Ar, Ai, Tk, state=(h, b))
+        y_t, (h_t, b_t) = hip_step(dt, u, Bc, Cc, Ar, Ai, Tk, torch.zeros(D, device=dev), (h, b))
+    torch.cuda.synchronize()
+    assert torch.equal(y_t, y_s[:, 0]) and torch.equal(h_t, h_s) and torch.equal(b_t, b_s)
+
+
 @pytest.mark.parametrize("case", range(8 * SCALE))
 def test_step_bcnorm_sweep(gpu_lib, case):
     """The step from raw B / C projections (BCNorm + p-sum inside the step, or
