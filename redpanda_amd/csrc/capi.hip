@@ -146,7 +146,7 @@ Plan make_plan(const rp_scan_args* a) {
   pl.S = S;
   pl.NPL = NPL;
   pl.CB = rp::kWaves * (rp::kWave / S);
-  pl.gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
+  pl.gk = rp::gate_code_all(a->A_imag != nullptr, a->NR, a->N, S, NPL);
   pl.ntiles = (int)((a->D + pl.CB - 1) / pl.CB);
   const int64_t nchunks = (a->L + rp::kCkptK - 1) / rp::kCkptK;
   pl.nck = (int)(nchunks > 0 ? nchunks - 1 : 0);
@@ -577,7 +577,7 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
   p.ntiles = (int)((a->D + CB - 1) / CB);
   if ((int64_t)p.ntiles * a->R > kI32Max)
     return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
-  const int gk = rp::gate_code(a->A_imag != nullptr, a->NR, S, NPL);
+
   // the tile kernel moves each channel's (h, beta) as 16-byte vectors (with
   // pad states when N is below the shape's S * NPL)
   const bool tile = a->N % 4 == 0 && rp::step_tile_shape(S, NPL) &&
@@ -613,11 +613,9 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
       return fail(RP_ERR_UNSUPPORTED, "step: grid too large");
   }
   // the tile kernel's all-rotational gate kind: no slot's split decided at
-  // run time (the default configurations: d_state 32 and 64, no tracking)
-  const int gk_launch = (tile && a->A_imag != nullptr && a->NR == (int64_t)S * NPL &&
-                         a->N == a->NR)
-                            ? rp::kGateRotAll
-                            : gk;
+  // run time (the default configurations: d_state 32 and 64, no tracking);
+  // the lane-layout kernel takes RotLead for it
+  const int gk_launch = rp::gate_code_all(a->A_imag != nullptr, a->NR, a->N, S, NPL);
   // (the prologue's BCNorm takes a state per lane: d_state <= 64)
   if (bn != nullptr && tile && p.ri == 1 && a->N <= rp::kWave) {
     p.bn_fused = 1;

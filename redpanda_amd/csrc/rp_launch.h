@@ -222,13 +222,26 @@ enum GateCode {
   kGateRotLead = 1,   // complex gates, slots j < NPL-1 rotational (NR >= S*(NPL-1))
   kGateRotTrack = 2,  // complex gates, slots j < NPL-1 rotational, slot NPL-1
                       // tracking or padding (NR == S*(NPL-1))
-  kGateRotAll = 3,    // step tile kernel only: complex gates, every slot
-                      // rotational (NR == N == S*NPL)
+  kGateRotAll = 3,    // complex gates, every slot rotational (NR == N == S*NPL):
+                      // instantiated for the step tile kernel and the scan
+                      // kernels of rot_all_scan_shape; elsewhere RotLead
 };
+
+// The lane shapes whose whole-tile scan kernels also take the all-rotational
+// gate kind: the reference's default d_state 32 (8 x 4) and 64 (16 x 4).
+constexpr bool rot_all_scan_shape(int S, int NPL) {
+  return NPL == 4 && (S == 8 || S == 16);
+}
 
 inline int gate_code(bool has_imag, int64_t NR, int S, int NPL) {
   if (!has_imag || NR < (int64_t)S * (NPL - 1)) return kGateGeneric;
   return NR == (int64_t)S * (NPL - 1) ? kGateRotTrack : kGateRotLead;
+}
+// The gate kind with the all-rotational case (every state rotational, no pad
+// slot) told apart.
+inline int gate_code_all(bool has_imag, int64_t NR, int64_t N, int S, int NPL) {
+  if (has_imag && NR == N && N == (int64_t)S * NPL) return kGateRotAll;
+  return gate_code(has_imag, NR, S, NPL);
 }
 
 hipError_t launch_scan_fwd(int S, int NPL, int gk, const ScanParams& p, const FwdOut& o,

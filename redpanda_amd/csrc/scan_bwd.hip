@@ -103,7 +103,7 @@ hipError_t launch_scan_bwd(int S, int NPL, int gk, const ScanParams& p, const Bw
   if (io.tpw > 1) return launch_scan_bwd_walk(S, NPL, gk, false, p, io, st);
 #define RP_CASE(SS, NN)                                                              \
   if (S == SS && NN == NPL)                                                          \
-    return with_gate_kind<NN>(gk, [&](auto g) {                                      \
+    return with_gate_kind_scan<SS, NN>(gk, [&](auto g) {                                      \
       return launch_bwd_t<SS, NN, decltype(g)>(p, io, st);                           \
     });
   RP_FOR_EACH_SHAPE(RP_CASE)

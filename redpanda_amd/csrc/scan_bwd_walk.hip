@@ -19,7 +19,7 @@ hipError_t launch_scan_bwd_walk(int S, int NPL, int gk, bool fast, const ScanPar
                                 const BwdIO& io, hipStream_t st) {
 #define RP_CASE(SS, NN)                                                              \
   if (S == SS && NN == NPL)                                                          \
-    return with_gate_kind<NN>(gk, [&](auto g) {                                      \
+    return with_gate_kind_scan<SS, NN>(gk, [&](auto g) {                                      \
       return fast ? launch_bwd_walk_t<SS, NN, decltype(g), true>(p, io, st)          \
                   : launch_bwd_walk_t<SS, NN, decltype(g), false>(p, io, st);        \
     });

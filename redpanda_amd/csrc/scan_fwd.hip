@@ -435,7 +435,7 @@ hipError_t launch_scan_fwd(int S, int NPL, int gk, const ScanParams& p, const Fw
                            hipStream_t st) {
 #define RP_CASE(SS, NN)                                                              \
   if (S == SS && NN == NPL)                                                          \
-    return with_gate_kind<NN>(gk, [&](auto g) {                                      \
+    return with_gate_kind_scan<SS, NN>(gk, [&](auto g) {                                      \
       return launch_fwd_t<SS, NN, decltype(g)>(p, o, st);                            \
     });
   RP_FOR_EACH_SHAPE(RP_CASE)

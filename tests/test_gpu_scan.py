@@ -197,10 +197,21 @@ def test_channel_counts(gpu_lib, D):
 
 @pytest.mark.parametrize("NR,NT,cplx", [(1, 0, True), (0, 3, True), (16, 0, False), (12, 4, True),
                                         (30, 10, True), (32, 8, True), (16, 4, True),
-                                        (56, 8, True), (64, 8, True), (120, 8, True)])
+                                        (56, 8, True), (64, 8, True), (120, 8, True),
+                                        (32, 0, True), (64, 0, True)])
 def test_state_splits(gpu_lib, NR, NT, cplx):
     c = make_case(300 + NR * 7 + NT, B=2, L=40, D=48, NR=NR, NT=NT, complex_=cplx)
     compare(c, False, f"NR={NR} NT={NT} complex={cplx}")
+
+
+@pytest.mark.parametrize("N", [32, 64])
+@pytest.mark.parametrize("bidir", [False, True])
+def test_all_rotational_whole_tiles(gpu_lib, N, bidir):
+    """Every state rotational at d_state 32 and 64 (the reference's default
+    configurations) over whole channel tiles: the whole-tile kernels'
+    all-rotational instantiation against the oracle."""
+    c = make_case(700 + N, B=2, L=37, D=64, NR=N, NT=0)
+    compare(c, bidir, f"all rotational N={N} bidirectional={bidir}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -367,7 +378,7 @@ STORAGE = {
 }
 
 
-@pytest.mark.parametrize("N,NT", [(20, 4), (40, 8), (72, 8)])
+@pytest.mark.parametrize("N,NT", [(20, 4), (40, 8), (72, 8), (32, 0), (64, 0)])
 @pytest.mark.parametrize("storage", sorted(STORAGE))
 @pytest.mark.parametrize("bidir", [False, True])
 def test_whole_tile_paths_equal_partial_tile(gpu_lib, N, NT, storage, bidir):
@@ -391,7 +402,7 @@ def test_whole_tile_paths_equal_partial_tile(gpu_lib, N, NT, storage, bidir):
     for k in ("delta", "u", "dy"):
         part[k] = c[k][:, :, :CB - 1].contiguous()
     for k in ("Ar", "Ai", "Tk"):
-        part[k] = c[k][:CB - 1].contiguous()
+        part[k] = None if c[k] is None else c[k][:CB - 1].contiguous()
     y1, g1 = hip_capi.scan_fwd_bwd(c, bidir, softplus=softplus)
     y2, g2 = hip_capi.scan_fwd_bwd(part, bidir, softplus=softplus)
     same = lambda a, b: torch.equal(a.view(torch.int32), b.view(torch.int32))
@@ -399,7 +410,8 @@ def test_whole_tile_paths_equal_partial_tile(gpu_lib, N, NT, storage, bidir):
     for k in ("delta", "u"):
         assert same(g1[k][:, :, :CB - 1].contiguous(), g2[k]), k
     for k in ("Ar", "Ai", "Tk"):
-        assert same(g1[k][:CB - 1].contiguous(), g2[k]), k
+        if g1[k] is not None:
+            assert same(g1[k][:CB - 1].contiguous(), g2[k]), k
     if not bidir:
         _, _, (h1, b1), keep1 = hip_capi.scan_fwd(c, with_state=True, softplus=softplus)
         _, _, (h2, b2), keep2 = hip_capi.scan_fwd(part, with_state=True, softplus=softplus)
