@@ -399,8 +399,9 @@ __device__ __forceinline__ bool is_rot(int j, int s, int NR) {
 }
 
 // Host side: calls f(GK{}) with the GateKind instantiation of gate code gk.
-// (kGateRotAll takes the RotLead instantiation here: the same values; the
-// launchers that instantiate it test for it first.)
+// (kGateRotAll takes the RotLead instantiation here, kGateRealAll the
+// Generic one: the same values; the launchers that instantiate them test for
+// them first.)
 template <int NPL, class F>
 hipError_t with_gate_kind(int gk, F&& f) {
   if (gk == kGateRotTrack) return f(GateKind<NPL - 1, 1, NPL - 1>{});
@@ -408,12 +409,13 @@ hipError_t with_gate_kind(int gk, F&& f) {
   return f(GateKind<0, 2, NPL>{});
 }
 
-// The scan launchers' dispatch: with_gate_kind, plus the all-rotational
-// instantiation on the shapes of rot_all_scan_shape.
+// The scan launchers' dispatch: with_gate_kind, plus the all-rotational and
+// all-real instantiations on the shapes of all_gate_shape.
 template <int S, int NPL, class F>
 hipError_t with_gate_kind_scan(int gk, F&& f) {
-  if constexpr (rot_all_scan_shape(S, NPL)) {
+  if constexpr (all_gate_shape(S, NPL)) {
     if (gk == kGateRotAll) return f(GateKind<NPL, 1, NPL>{});
+    if (gk == kGateRealAll) return f(GateKind<NPL, 0, NPL>{});
   }
   return with_gate_kind<NPL>(gk, f);
 }

@@ -224,23 +224,28 @@ enum GateCode {
                       // tracking or padding (NR == S*(NPL-1))
   kGateRotAll = 3,    // complex gates, every slot rotational (NR == N == S*NPL):
                       // instantiated for the step tile kernel and the scan
-                      // kernels of rot_all_scan_shape; elsewhere RotLead
+                      // kernels of all_gate_shape; elsewhere RotLead
+  kGateRealAll = 4,   // real decay (no A_imag), every slot decaying (NR == N ==
+                      // S*NPL): instantiated for all_gate_shape; elsewhere
+                      // Generic
 };
 
-// The lane shapes whose whole-tile scan kernels also take the all-rotational
-// gate kind: the reference's default d_state 32 (8 x 4) and 64 (16 x 4).
-constexpr bool rot_all_scan_shape(int S, int NPL) {
-  return NPL == 4 && (S == 8 || S == 16);
+// The lane shapes whose kernels also take the all-rotational and all-real
+// gate kinds: 4 slots of 4, 8 or 16 lanes, d_state 16, 32 and 64 (the
+// reference's default d_state 32 and 64, and its CPU configuration's real
+// d_state 16).
+constexpr bool all_gate_shape(int S, int NPL) {
+  return NPL == 4 && (S == 4 || S == 8 || S == 16);
 }
 
 inline int gate_code(bool has_imag, int64_t NR, int S, int NPL) {
   if (!has_imag || NR < (int64_t)S * (NPL - 1)) return kGateGeneric;
   return NR == (int64_t)S * (NPL - 1) ? kGateRotTrack : kGateRotLead;
 }
-// The gate kind with the all-rotational case (every state rotational, no pad
-// slot) told apart.
+// The gate kind with the all-rotational and all-real cases (every state
+// rotational or decaying, no pad slot) told apart.
 inline int gate_code_all(bool has_imag, int64_t NR, int64_t N, int S, int NPL) {
-  if (has_imag && NR == N && N == (int64_t)S * NPL) return kGateRotAll;
+  if (NR == N && N == (int64_t)S * NPL) return has_imag ? kGateRotAll : kGateRealAll;
   return gate_code(has_imag, NR, S, NPL);
 }
 

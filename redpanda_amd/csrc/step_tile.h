@@ -316,12 +316,17 @@ hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
 }
 
 // The tile kernel for shape (S, NPL), with or without pad states; without,
-// also the all-rotational gate kind (no slot decided at run time).
+// also the all-rotational gate kind (no slot decided at run time) and, on
+// all_gate_shape, the all-real one.
 template <int S, int NPL, bool PAD>
 hipError_t launch_step_tile(int gk, const StepParams& p, hipStream_t st) {
   if constexpr (step_tile_shape(S, NPL) && (!PAD || step_tile_split(S) > 1)) {
     if constexpr (!PAD) {
       if (gk == kGateRotAll) return launch_step_tile_t<S, NPL, GateKind<NPL, 1, NPL>, PAD>(p, st);
+      if constexpr (all_gate_shape(S, NPL)) {
+        if (gk == kGateRealAll)
+          return launch_step_tile_t<S, NPL, GateKind<NPL, 0, NPL>, PAD>(p, st);
+      }
     }
     return with_gate_kind<NPL>(gk, [&](auto g) {
       return launch_step_tile_t<S, NPL, decltype(g), PAD>(p, st);

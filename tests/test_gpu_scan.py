@@ -204,14 +204,16 @@ def test_state_splits(gpu_lib, NR, NT, cplx):
     compare(c, False, f"NR={NR} NT={NT} complex={cplx}")
 
 
-@pytest.mark.parametrize("N", [32, 64])
+@pytest.mark.parametrize("N", [16, 32, 64])
 @pytest.mark.parametrize("bidir", [False, True])
-def test_all_rotational_whole_tiles(gpu_lib, N, bidir):
-    """Every state rotational at d_state 32 and 64 (the reference's default
-    configurations) over whole channel tiles: the whole-tile kernels'
-    all-rotational instantiation against the oracle."""
-    c = make_case(700 + N, B=2, L=37, D=64, NR=N, NT=0)
-    compare(c, bidir, f"all rotational N={N} bidirectional={bidir}")
+@pytest.mark.parametrize("cplx", [True, False])
+def test_all_rotational_whole_tiles(gpu_lib, N, bidir, cplx):
+    """Every state rotational (complex) or decaying (real) at d_state 16, 32
+    and 64 (the reference's default configurations and its CPU one) over
+    whole channel tiles: the whole-tile kernels' all-rotational and all-real
+    instantiations against the oracle."""
+    c = make_case(700 + N, B=2, L=37, D=64, NR=N, NT=0, complex_=cplx)
+    compare(c, bidir, f"all {'rotational' if cplx else 'real'} N={N} bidirectional={bidir}")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -49,7 +49,8 @@ def to(t):
                                         (40, 8, True), (48, 16, True), (64, 16, False),
                                         (20, 4, True), (72, 8, True), (20, 8, True),
                                         (40, 4, True), (56, 4, False), (80, 16, True),
-                                        (120, 8, True), (100, 16, True)])
+                                        (120, 8, True), (100, 16, True), (16, 0, False),
+                                        (64, 0, False), (32, 0, False)])
 @pytest.mark.parametrize("fresh", [False, True])
 def test_step_matches_reference_step(gpu_lib, NR, NT, cplx, fresh):
     hip_step = _step()
