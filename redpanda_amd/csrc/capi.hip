@@ -580,14 +580,17 @@ int step_impl(const rp_step_args* a, const rp_bcnorm_args* bn, void* stream) {
 
   // the tile kernel moves each channel's (h, beta) as 16-byte vectors (with
   // pad states when N is below the shape's S * NPL)
+  // (pad states only in the last slot, or anywhere with two slices per
+  // thread, whose vectors are checked one by one)
   const bool tile = a->N % 4 == 0 && rp::step_tile_shape(S, NPL) &&
-                    (a->N == S * NPL || a->N > S * (NPL - 1)) &&
+                    (a->N == S * NPL || a->N > S * (NPL - 1) ||
+                     rp::step_tile_split(S, NPL) * 2 == S) &&
                     aligned(a->h_out, 16) &&
                     (a->h_in == nullptr || aligned(a->h_in, 16)) &&
                     (a->beta_rank1 || (aligned(a->beta_out, 16) &&
                                        (a->h_in == nullptr || aligned(a->beta_in, 16))));
   if (tile) {
-    const int tch = rp::kStepTile / rp::step_tile_split(S);
+    const int tch = rp::kStepTile / rp::step_tile_split(S, NPL);
     p.ctiles = (int)((a->D + tch - 1) / tch);
     // rollouts per workgroup: a few amortise the workgroup's prologue (gate
     // parameters, B / C rows) while keeping many workgroups in flight;

@@ -87,7 +87,7 @@ struct StepParams {
   float* beta_out;
   float* y;
   int ntiles;   // lane-layout kernel: channel tiles of CB
-  int ctiles;   // tile kernel: channel tiles of kStepTile / step_tile_split(S)
+  int ctiles;   // tile kernel: channel tiles of kStepTile / step_tile_split(S, NPL)
   int ri;       // tile kernel: rollouts per workgroup
   int rgroups;  // tile kernel: ceil(R / ri)
   // tile kernel, one rollout per workgroup: the B / C rows computed in the
@@ -195,10 +195,15 @@ constexpr int kStepTile = kThreads;
 // Threads per channel of the step tile kernel for S state slices: S / 4 from
 // 8 slices up (d_state 24-40 and 48-80), each thread taking 4 slices (one
 // float4 per slot); the tile then holds kStepTile / (S / 4) channels.
-constexpr int step_tile_split(int S) { return S >= 8 ? S / 4 : 1; }
-// Whether the step tile kernel takes the shape (S, NPL) (d_state a multiple
-// of 4 up to S * NPL, above S * (NPL - 1) when below S * NPL: pad states
-// only in the last slot).
+// At 8 slots of 16 slices (d_state 97-128) S / 2 threads of 2 slices each
+// (one float2 per slot), halving a thread's states.
+constexpr int step_tile_split(int S, int NPL) {
+  return (S == 16 && NPL == 8) ? S / 2 : S >= 8 ? S / 4 : 1;
+}
+// Whether the step tile kernel takes the shape (S, NPL): d_state a multiple
+// of 4 up to S * NPL; below S * NPL the host also asks for pad states only
+// in the last slot (above S * (NPL - 1)), except where a thread holds 2
+// slices (float2 per slot), which takes any pad pattern.
 constexpr bool step_tile_shape(int S, int NPL) {
   return S * NPL <= 40 || S == 16;
 }

@@ -64,18 +64,22 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   static_assert(FULLD || !SHARED, "the shared-state instantiation is for whole tiles");
   constexpr int NP = S * NPL;
   constexpr int NV = NP / 4;            // float4s per channel at N == NP
-  // SPL threads per channel: from 8 slices up (d_state 24-40, 44-128) a
+  // SPL threads per channel: from 8 slices up (d_state 24-40, 44-96) a
   // channel's states split between S / 4 adjacent lanes, 4 slices each (one
   // float4 per slot), so that the gate parameters and the states of a thread
   // fit the registers of several waves per SIMD (one thread per channel took
-  // 256 VGPRs, one wave per SIMD, at d_state 32 all rotational)
-  constexpr int SPL = step_tile_split(S);
+  // 256 VGPRs, one wave per SIMD, at d_state 32 all rotational); at 8 slots
+  // of 16 (d_state 97-128) between S / 2 lanes, 2 slices each (one float2
+  // per slot)
+  constexpr int SPL = step_tile_split(S, NPL);
   constexpr int SS = S / SPL;           // slices per thread
   constexpr int NPT = NP / SPL;         // states per thread
-  constexpr int NVT = NV / SPL;         // float4s per thread
-  static_assert(SPL == 1 || SS == 4, "a split thread holds one float4 per slot");
-  static_assert(SPL <= 4, "the y combine covers up to four threads per channel");
+  constexpr int NVT = NPL;              // vectors per thread: one per slot
+  using V = std::conditional_t<SS == 2, float2, float4>;
+  static_assert(SS == 4 || (SS == 2 && SPL > 1), "a thread holds one float4 or float2 per slot");
+  static_assert(SPL <= 8, "the y combine covers up to eight threads per channel");
   static_assert(!PAD || SPL > 1, "a one-thread channel (S == 4) has no pad float4s");
+  constexpr int VPC = NP / SS;          // vectors per channel at N == NP
   constexpr int TCH = kThreads / SPL;   // channels per workgroup
   constexpr int NB = TCH * NV / kThreads;  // float4s per thread when staging a block (at most)
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
@@ -94,10 +98,16 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   const int cld = cvalid ? c : p.D - 1;  // loads stay in bounds; only valid channels store
   const int N = p.N;                    // N == NP, or with PAD N < NP (checked by the host)
   const int NVM = PAD ? N / 4 : NV;     // float4s per channel row
-  // the thread's last-slot float4 lies in the row (N > S * (NPL - 1): pad
-  // states only ever fill part of the last slot; with SPL > 1 a thread's
-  // float4 of slot j is the channel's float4 j * SPL + half)
-  const bool last_in = !PAD || (NPL - 1) * SPL + (tid % SPL) < NVM;
+  const int VPM = PAD ? N / SS : VPC;   // vectors (V) per channel row
+  // whether the thread's vector of slot v lies in the row; a thread's vector
+  // of slot v is the channel's vector v * SPL + half.  With 4 slices per
+  // thread pad states only ever fill part of the last slot (N > S * (NPL -
+  // 1)), so only that vector is tested at run time; with 2, every one is
+  const bool last_in = !PAD || (NPL - 1) * SPL + (tid % SPL) < VPM;
+  auto in_row = [&](int v) {
+    if constexpr (SS == 2) return !PAD || v * SPL + (tid % SPL) < VPM;
+    return v < NVT - 1 || last_in;
+  };
   // float4s of the block
   const int nvalid = (FULLD && !PAD) ? TCH * NV : (FULLD ? TCH : min(TCH, p.D - c0)) * NVM;
   const bool has_imag = p.Ai != nullptr;
@@ -213,21 +223,23 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       }
     }
     __syncthreads();  // the block (and, the first time, the table and B / C rows)
-    // the thread's float4 v: the channel's float4 v * SPL + half; with PAD,
-    // beyond the row (pad states, only ever in the last slot) zeros
-    float4 h4[NVT], b4[NVT];
+    // the thread's vector v: the channel's vector v * SPL + half; with PAD,
+    // beyond the row (pad states) zeros
+    V* const sHv = reinterpret_cast<V*>(sH);
+    V* const sBv = reinterpret_cast<V*>(sBt);
+    V h4[NVT], b4[NVT];
 #pragma unroll
     for (int v = 0; v < NVT; ++v) {
       // read as values, then selected (an index past the row stays inside
       // the block's LDS); a select of the two places would load through a
       // generic pointer
-      const bool in_row = v < NVT - 1 || last_in;
-      const int k = cl * NVM + v * SPL + half;
-      h4[v] = sH[k];
-      if (!in_row) h4[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+      const bool row = in_row(v);
+      const int k = cl * VPM + v * SPL + half;
+      h4[v] = sHv[k];
+      if (!row) h4[v] = V{};
       if constexpr (!RANK1) {
-        b4[v] = sBt[k];
-        if (!in_row) b4[v] = make_float4(0.f, 0.f, 0.f, 0.f);
+        b4[v] = sBv[k];
+        if (!row) b4[v] = V{};
       }
     }
     const float* Bs = sBC[rr];
@@ -241,11 +253,11 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     for (int i = 0; i < NPT; ++i) {
       const int j = i / SS, ql = i % SS;
       const int n = st_n(i);
-      float& hs = (&h4[i / 4].x)[i % 4];
-      float& bs = (&b4[i / 4].x)[i % 4];
+      float& hs = (&h4[i / SS].x)[i % SS];
+      float& bs = (&b4[i / SS].x)[i % SS];
       // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
       // same bits as the product the full form stored (zero for a pad state)
-      const float hbp = RANK1 ? ((j < NPL - 1 || last_in) ? fmul(hdp, Bp[n]) : 0.f) : 0.5f * bs;
+      const float hbp = RANK1 ? (in_row(j) ? fmul(hdp, Bp[n]) : 0.f) : 0.5f * bs;
       const float g = gate_of<S, GK>(j, half * SS + ql, p.NR, has_imag, dt, pah[i], wh[i], sCos);
       const float hb = fmul(hd, Bs[n]);
       hs = ffma(g, hs, ffma(g, hbp, hb));  // fwd_update's form and rounding
@@ -259,6 +271,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     float ysum = tree_sum<SS>(ys);
     if constexpr (SPL >= 2) ysum = ysum + __shfl_xor(ysum, 1);
     if constexpr (SPL >= 4) ysum = ysum + __shfl_xor(ysum, 2);
+    if constexpr (SPL >= 8) ysum = ysum + __shfl_xor(ysum, 4);
     if (cvalid && half == 0) {
       float yv = ysum + fmul(uu, dsk);
       if (p.z != nullptr) yv = silu_gate(yv, zz, p.dt_z);
@@ -270,9 +283,9 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     }
 #pragma unroll
     for (int v = 0; v < NVT; ++v) {
-      if (v < NVT - 1 || last_in) {
-        sH[cl * NVM + v * SPL + half] = h4[v];
-        if constexpr (!RANK1) sBt[cl * NVM + v * SPL + half] = b4[v];
+      if (in_row(v)) {
+        sHv[cl * VPM + v * SPL + half] = h4[v];
+        if constexpr (!RANK1) sBv[cl * VPM + v * SPL + half] = b4[v];
       }
     }
     __syncthreads();  // the updated block
@@ -293,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 template <int S, int NPL, class GK, bool DSP, bool RANK1, bool PAD>
 hipError_t launch_step_tile_d(const StepParams& p, hipStream_t st) {
   dim3 grid((unsigned)((int64_t)p.ctiles * p.rgroups));
-  const int tch = kThreads / step_tile_split(S);
+  const int tch = kThreads / step_tile_split(S, NPL);
   if (p.D % tch == 0 && p.ssr == 0)
     hipLaunchKernelGGL((step_tile_kernel<S, NPL, GK, true, DSP, RANK1, true, PAD>), grid,
                        dim3(kThreads), 0, st, p);
@@ -320,7 +333,7 @@ hipError_t launch_step_tile_t(const StepParams& p, hipStream_t st) {
 // all_gate_shape, the all-real one.
 template <int S, int NPL, bool PAD>
 hipError_t launch_step_tile(int gk, const StepParams& p, hipStream_t st) {
-  if constexpr (step_tile_shape(S, NPL) && (!PAD || step_tile_split(S) > 1)) {
+  if constexpr (step_tile_shape(S, NPL) && (!PAD || step_tile_split(S, NPL) > 1)) {
     if constexpr (!PAD) {
       if (gk == kGateRotAll) return launch_step_tile_t<S, NPL, GateKind<NPL, 1, NPL>, PAD>(p, st);
       if constexpr (all_gate_shape(S, NPL)) {
