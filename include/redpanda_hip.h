@@ -304,6 +304,13 @@ int rp_rmsnorm_check(const rp_rmsnorm_args* a);
  * pass; replaces x + out and RMSNorm's five elementwise and reduction ops. */
 int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream);
 
+/* softplus(x) of n fp32 values (engine/mamba.py:300: F.softplus of the dt
+ * projection, beta 1, threshold 20), with the same bits as the scan's and
+ * the step's softplus on load (delta_softplus): for a caller that builds a
+ * rank-1 beta row [softplus(x) u | B] itself (engine/mamba.py:480-481) and
+ * needs it to match the full beta the kernels write.  out may equal x. */
+int rp_softplus(const float* x, float* out, int64_t n, void* stream);
+
 /*
  * Host boundary of one lockstep rollout ply.  The reference moves each
  * rollout's continuation row (engine/mars_search.py:262, _select_move's

@@ -137,6 +137,7 @@ SIGNATURES = {
     "rp_step_bcnorm": (ctypes.c_int, [ctypes.POINTER(StepArgs), ctypes.POINTER(BcNormArgs), _vp]),
     "rp_rmsnorm_check": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs)]),
     "rp_rmsnorm_fwd": (ctypes.c_int, [ctypes.POINTER(RmsNormArgs), _vp]),
+    "rp_softplus": (ctypes.c_int, [_vp, _vp, _i64, _vp]),
     "rp_ply_topk_check": (ctypes.c_int, [ctypes.POINTER(PlyTopkArgs)]),
     "rp_ply_topk": (ctypes.c_int, [ctypes.POINTER(PlyTopkArgs), _vp]),
     "rp_ply_gather_check": (ctypes.c_int, [ctypes.POINTER(PlyGatherArgs)]),

@@ -1014,6 +1014,14 @@ int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream) {
   return RP_OK;
 }
 
+int rp_softplus(const float* x, float* out, int64_t n, void* stream) {
+  if (n < 0) return fail(RP_ERR_INVALID, "softplus: n < 0");
+  if (n > 0 && (x == nullptr || out == nullptr)) return fail(RP_ERR_INVALID, "softplus: NULL buffer");
+  hipError_t e = rp::launch_softplus(x, out, n, (hipStream_t)stream);
+  if (e != hipSuccess) return fail_hip(e, "softplus launch");
+  return RP_OK;
+}
+
 int rp_ply_topk_check(const rp_ply_topk_args* a) {
   if (a == nullptr) return fail(RP_ERR_INVALID, "ply topk args: NULL");
   if (a->R < 0 || a->V < 1) return fail(RP_ERR_INVALID, "ply topk args: R < 0 or V < 1");

@@ -164,9 +164,39 @@ __device__ __forceinline__ uint32_t load_raw_byte(const void* base, uint32_t off
 
 __device__ __forceinline__ float fmul(float a, float b) { return a * b; }
 
-// delta = softplus(x) as torch computes it for the dt projection
-// (engine/mamba.py:300, F.softplus with beta 1, threshold 20, in fp32).
-__device__ __forceinline__ float softplus_of(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+// delta = softplus(x) for the dt projection (engine/mamba.py:300, F.softplus
+// with beta 1, threshold 20, in fp32), as max(x, 0) + log1p(t), t = exp(-|x|)
+// in (0, 1].  log1p from the series log1p(t) = 2 atanh(s) = 2 (s + s^3/3 +
+// s^5/5 + ...), s = t / (2 + t) <= 1/3 (Abramowitz & Stegun 4.1.27): the
+// terms through s^15 leave a truncation below 3e-9 relative.  s from the
+// reciprocal with one Newton step against the exact denominator (2 + t
+// rounds to d, and t - (d - 2) is its rounding error, exact).  About 30 VALU
+// where log1pf's double-float evaluation takes about 110; within 2.8 ulp of
+// the exact value (log1pf(expf(x)) in fp32 is within 2.7: the rounding of
+// exp's result dominates both).  Explicit FMAs and no contraction: every
+// kernel rounds it the same way.
+__device__ __forceinline__ float softplus_of(float x) {
+#pragma clang fp contract(off)
+  const float t = expf(-fabsf(x));
+  const float d = 2.f + t;
+  const float dlo = t - (d - 2.f);
+  const float r = __builtin_amdgcn_rcpf(d);
+  const float s0 = t * r;
+  float e = __builtin_fmaf(-s0, d, t);
+  e = __builtin_fmaf(-s0, dlo, e);
+  const float s = __builtin_fmaf(e, r, s0);
+  const float s2 = s * s;
+  float q = 1.f / 15.f;
+  q = __builtin_fmaf(q, s2, 1.f / 13.f);
+  q = __builtin_fmaf(q, s2, 1.f / 11.f);
+  q = __builtin_fmaf(q, s2, 1.f / 9.f);
+  q = __builtin_fmaf(q, s2, 1.f / 7.f);
+  q = __builtin_fmaf(q, s2, 1.f / 5.f);
+  q = __builtin_fmaf(q, s2, 1.f / 3.f);
+  const float l = __builtin_fmaf(2.f * (s * s2), q, 2.f * s);
+  const float v = fmaxf(x, 0.f) + l;
+  return x > 20.f ? x : v;
+}
 
 // fp32 -> the value a storage dtype holds (round to nearest even, as torch
 // converts); inf and nan pass through.

@@ -188,6 +188,7 @@ struct RmsNormParams {
 };
 
 hipError_t launch_rmsnorm_fwd(const RmsNormParams& p, hipStream_t st);
+hipError_t launch_softplus(const float* x, float* out, int64_t n, hipStream_t st);
 
 // Channels (one per thread) of the step tile kernel's workgroup, and the
 // most rollouts one of its workgroups walks.

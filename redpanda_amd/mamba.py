@@ -37,7 +37,7 @@ from redpanda_amd.bcnorm import hip_bcnorm_psum
 from redpanda_amd.mixer import hip_mixer_out
 from redpanda_amd.norm import hip_add_rmsnorm
 from redpanda_amd.scan import hip_scan_with_state, hip_trapezoidal_scan
-from redpanda_amd.step import compact_beta, full_beta, hip_step, is_compact
+from redpanda_amd.step import compact_beta, full_beta, hip_softplus, hip_step, is_compact
 
 # Chunk length of the reference's streaming scan (engine/mamba.py:101); kept
 # as a module constant for callers that read it.  The HIP scan is not chunked.
@@ -296,8 +296,8 @@ class Mamba3Block(nn.Module):
     @staticmethod
     def _compact_beta(x_dt, u, Bc):
         """Rank-1 row [dt*u | B] of one token's beta, dt = softplus(x_dt) in
-        fp32 as the kernels compute it (differentiable torch ops)."""
-        dtu = F.softplus(x_dt.float()) * u.float()
+        fp32 with the kernels' bits (differentiable)."""
+        dtu = hip_softplus(x_dt) * u.float()
         return compact_beta(dtu, Bc)
 
     # ── O(1) step (engine/mamba.py:427-498) ──

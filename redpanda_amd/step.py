@@ -52,6 +52,35 @@ def compact_beta(dtu, Bc):
     return torch.cat([dtu.to(torch.float32), Bc.to(torch.float32)], dim=-1)
 
 
+class _Softplus(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        xf = x.detach().to(torch.float32).contiguous()
+        out = torch.empty_like(xf)
+        lib = _lib.load()
+        _lib.check(lib.rp_softplus(xf.data_ptr(), out.data_ptr(), xf.numel(),
+                                   _lib.stream_of(xf.device)), lib)
+        ctx.save_for_backward(xf)
+        ctx.in_dtype = x.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        # torch's softplus backward: g z / (z + 1), z = exp(x); g above 20
+        (xf,) = ctx.saved_tensors
+        z = torch.exp(xf)
+        return torch.where(xf > 20.0, g, g * z / (z + 1.0)).to(ctx.in_dtype)
+
+
+def hip_softplus(x):
+    """fp32 softplus(x) of the dt projection (engine/mamba.py:300) with the
+    bits the scan and step kernels compute on load (delta_softplus), for
+    rank-1 beta rows built on the host; differentiable (d/dx = sigmoid(x))."""
+    if not x.is_cuda:
+        raise RuntimeError("hip_softplus: x must be on a ROCm device")
+    return _Softplus.apply(x)
+
+
 def full_beta(bp, D):
     """The (R, D, N) beta of rank-1 rows bp (R, D + N): (dt*u)[:, :, None] * B[:, None, :]."""
     return bp[..., :D, None] * bp[..., None, D:]

@@ -112,6 +112,14 @@ def test_bwd_workspace_too_small_rejected(lib):
     assert lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), None) == -4
 
 
+def test_softplus_argument_checks(lib):
+    # rejected before any launch; n = 0 launches nothing
+    assert lib.rp_softplus(None, None, -1, None) < 0
+    assert "n < 0" in lib.rp_last_error().decode()
+    assert lib.rp_softplus(None, 0x10000, 8, None) < 0
+    assert lib.rp_softplus(None, None, 0, None) == 0
+
+
 def _step_args(**kw):
     a = _lib.StepArgs()
     a.R, a.D, a.N, a.NR, a.NT = 16, 64, 20, 16, 4

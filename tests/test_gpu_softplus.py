@@ -15,7 +15,7 @@ import torch
 import torch.nn.functional as F
 
 from redpanda_amd.scan import hip_scan_with_state, hip_trapezoidal_scan
-from redpanda_amd.step import hip_step
+from redpanda_amd.step import hip_softplus, hip_step
 
 pytestmark = pytest.mark.gpu
 dev = "cuda"
@@ -123,3 +123,49 @@ def test_inference_forward_equals_training_forward(gpu_lib, bidirectional):
                                 delta_softplus=True)
     torch.cuda.synchronize()
     assert torch.equal(y_inf, y_tr.detach())
+
+
+def _ulp_err(v, ref64):
+    """|v - ref| in units of the fp32 spacing at ref (float64 arithmetic)."""
+    import numpy as np
+    r32 = ref64.astype(np.float32)
+    return np.abs(v.astype(np.float64) - ref64) / np.spacing(np.abs(r32))
+
+
+def test_softplus_bits_against_float64(gpu_lib):
+    """The kernels' softplus itself, read out exactly: one step from a fresh
+    state with u = 1, B = C = 1 on the first state (0 on the others) and no
+    skip term gives h = (delta * u / 2) B and y = C h = delta / 2
+    (engine/mamba.py:481-494 with h = beta_prev = 0), so 2y is the kernel's
+    delta bit for bit.  Against float64's log1p(exp(x)): within 3 ulp
+    (fp32's log1pf(expf(x)) is within 2.7: the rounding of exp's result
+    dominates both), and x itself above the threshold 20."""
+    import numpy as np
+    R, D, NT = 64, 1024, 4
+    g = torch.Generator().manual_seed(77)
+    x = torch.cat([torch.rand(R * D // 2, generator=g) * 100 - 80,      # (-80, 20)
+                   torch.randn(R * D // 4, generator=g) * 2,            # the knee
+                   torch.randn(R * D // 4, generator=g) * 1e-3])
+    x[:8] = torch.tensor([20.0, 20.000002, 19.999998, 0.0, -0.0, 25.0, -80.0, 1e-30])
+    x = x.view(R, D).to(dev)
+    u = torch.ones(R, D, device=dev)
+    bc = torch.zeros(R, NT, device=dev)
+    bc[:, 0] = 1.0
+    Tk = torch.full((D, NT), 0.5, device=dev)
+    Dk = torch.zeros(D, device=dev)
+    y, _ = hip_step(x, u, bc, bc.clone(), None, None, Tk, Dk, None, delta_softplus=True)
+    torch.cuda.synchronize()
+    delta = (2.0 * y).cpu().numpy().astype(np.float32)
+    xs = x.cpu().numpy()
+    xd = xs.astype(np.float64)
+    above = xs > 20.0
+    ref = np.where(above, xd, np.log1p(np.exp(np.minimum(xd, 20.0))))
+    assert np.array_equal(delta[above], xs[above])
+    # the standalone pass (rank-1 beta rows built on the host) has the same bits
+    assert np.array_equal(hip_softplus(x).cpu().numpy(), delta)
+    err = _ulp_err(delta[~above], ref[~above])
+    err_torch = _ulp_err(F.softplus(x).cpu().numpy(), ref)[~above]
+    print(f"[softplus bits] max {err.max():.2f} ulp (torch fp32 {err_torch.max():.2f}), "
+          f"mean {err.mean():.3f} ({err_torch.mean():.3f}), equal to torch "
+          f"{float((delta == F.softplus(x).cpu().numpy()).mean()):.4f}", flush=True)
+    assert err.max() <= 3.0
