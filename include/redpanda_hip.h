@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RP_ABI_VERSION 12
+#define RP_ABI_VERSION 13
 
 /* element type codes of the streamed scan inputs (delta, u, Bc, Cc); each
  * tensor carries its own code, as autocast hands over mixed dtypes */
@@ -58,6 +58,12 @@ enum {
  * delta_softplus = 1: delta holds the dt projection x and the scan runs on
  * softplus(x) as engine/mamba.py:300 computes it (F.softplus, beta 1,
  * threshold 20, fp32); rp_scan_bwd's d_delta is then the gradient of x.
+ * grad_in_storage = 1: rp_scan_bwd writes d_delta and d_u in delta's and
+ * u's storage dtypes (rounded to nearest even, as torch converts its fp32
+ * result), instead of fp32: autograd returns input gradients in the input's
+ * dtype, and the conversion passes over (B, L, D) then disappear.  A
+ * bidirectional scan then also keeps its first direction's fp32 partial
+ * sums in the backward's workspace (rp_scan_bwd_work_bytes counts them).
  */
 typedef struct rp_scan_args {
   int64_t B, L, D, N, NR, NT;
@@ -73,6 +79,7 @@ typedef struct rp_scan_args {
   const float* track;
   const float* h0;
   const float* beta0;
+  int32_t grad_in_storage;  /* 0: fp32 d_delta / d_u; 1: see above           */
 } rp_scan_args;
 
 /*
@@ -93,7 +100,8 @@ typedef struct rp_scan_fwd_out {
 
 /*
  * Backward.  dy: (B, L, D) fp32 contiguous upstream gradient of y.  ckpt:
- * the workspace the matching forward filled.  Outputs, fp32 contiguous:
+ * the workspace the matching forward filled.  Outputs, contiguous, fp32
+ * (d_delta and d_u in delta's and u's dtypes with grad_in_storage):
  * d_delta, d_u (B, L, D); d_Bc, d_Cc (B, L, N); d_A_real, d_A_imag (D, NR)
  * (d_A_imag ignored when A_imag is NULL); d_track (D, NT).  work:
  * rp_scan_bwd_work_bytes() of scratch.  dh_last, dbeta_last: NULL, or
@@ -112,8 +120,8 @@ typedef struct rp_scan_bwd_io {
   const float* ckpt;
   const float* dh_last;
   const float* dbeta_last;
-  float* d_delta;
-  float* d_u;
+  void* d_delta;   /* fp32, or delta's dtype with grad_in_storage */
+  void* d_u;       /* fp32, or u's dtype with grad_in_storage     */
   float* d_Bc;
   float* d_Cc;
   float* d_A_real;

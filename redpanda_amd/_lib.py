@@ -13,7 +13,7 @@ import torch
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libredpanda_hip.so")
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 RP_F32, RP_BF16, RP_F16 = 0, 1, 2
 DTYPE_CODES = {torch.float32: RP_F32, torch.bfloat16: RP_BF16, torch.float16: RP_F16}
 MAX_STATE = 128
@@ -33,6 +33,7 @@ class ScanArgs(ctypes.Structure):
         ("Bc", _vp), ("Bc_sb", _i64), ("Bc_sl", _i64),
         ("Cc", _vp), ("Cc_sb", _i64), ("Cc_sl", _i64),
         ("A_real", _vp), ("A_imag", _vp), ("track", _vp), ("h0", _vp), ("beta0", _vp),
+        ("grad_in_storage", _i32),
     ]
 
 

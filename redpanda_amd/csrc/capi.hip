@@ -81,6 +81,7 @@ struct Plan {
   int S, NPL, CB, ntiles, nck, ndir, bg, nbg, tpw, ntg;
   int gk;     // gate kind: rotational / tracking split fixed at compile time
   int64_t ckpt_bytes, part_bc_bytes, part_par_bytes;
+  int64_t pd_bytes;    // the first direction's fp32 (d_delta, d_u) sums, when the outputs are 16-bit
   int64_t dcache_off;  // byte offset of the softplus(x) cache in the workspace, or -1
 };
 
@@ -106,6 +107,8 @@ int scan_validate(const rp_scan_args* a) {
     return fail(RP_ERR_INVALID, "scan args: delta_softplus must be 0 or 1");
   if (a->bidirectional != 0 && a->bidirectional != 1)
     return fail(RP_ERR_INVALID, "scan args: bidirectional must be 0 or 1");
+  if (a->grad_in_storage != 0 && a->grad_in_storage != 1)
+    return fail(RP_ERR_INVALID, "scan args: grad_in_storage must be 0 or 1");
   const int64_t work = a->B * a->L;
   if (work > 0 && a->D > 0) {
     if (!a->delta || !a->u || !a->Bc || !a->Cc)
@@ -184,6 +187,9 @@ Plan make_plan(const rp_scan_args* a) {
   }
   pl.part_bc_bytes = round_up(2 * (int64_t)pl.ntg * a->B * a->L * a->N * 4, 256);
   pl.part_par_bytes = round_up((int64_t)pl.nbg * 2 * a->D * a->N * 8, 256);
+  pl.pd_bytes = 0;
+  if (a->grad_in_storage && pl.ndir == 2 && (a->dtype_delta != RP_F32 || a->dtype_u != RP_F32))
+    pl.pd_bytes = round_up(2 * a->B * a->L * a->D * 4, 256);
   return pl;
 }
 
@@ -278,7 +284,7 @@ int64_t rp_scan_ckpt_bytes(const rp_scan_args* a) {
 int64_t rp_scan_bwd_work_bytes(const rp_scan_args* a) {
   if (scan_validate(a) != RP_OK) return -1;
   const Plan pl = make_plan(a);
-  return pl.part_bc_bytes + pl.part_par_bytes;
+  return pl.part_bc_bytes + pl.part_par_bytes + pl.pd_bytes;
 }
 
 int rp_scan_fwd(const rp_scan_args* a, const rp_scan_fwd_out* out, void* stream) {
@@ -374,11 +380,15 @@ int scan_bwd_impl(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream,
   if (st != RP_OK) return st;
   if (io == nullptr) return fail(RP_ERR_INVALID, "scan bwd: NULL io block");
   const Plan pl = make_plan(a);
-  const int64_t need = pl.part_bc_bytes + pl.part_par_bytes;
+  const int64_t need = pl.part_bc_bytes + pl.part_par_bytes + pl.pd_bytes;
   const int64_t work = a->B * a->L * a->D;
+  const int dt_dd = a->grad_in_storage ? a->dtype_delta : RP_F32;
+  const int dt_du = a->grad_in_storage ? a->dtype_u : RP_F32;
   if (work > 0) {
     if (!io->dy || !io->d_delta || !io->d_u)
       return fail(RP_ERR_INVALID, "scan bwd: NULL dy / d_delta / d_u");
+    if (!aligned(io->d_delta, elem_size(dt_dd)) || !aligned(io->d_u, elem_size(dt_du)))
+      return fail(RP_ERR_INVALID, "scan bwd: misaligned d_delta / d_u");
     if (pl.ckpt_bytes > 0 && (!io->ckpt || !aligned(io->ckpt, 256)))
       return fail(RP_ERR_INVALID,
                   "scan bwd: 256-byte aligned checkpoint workspace required for L=%lld",
@@ -430,8 +440,19 @@ int scan_bwd_impl(const rp_scan_args* a, const rp_scan_bwd_io* io, void* stream,
   b.d_beta0 = io->d_beta0;
   b.d_delta = io->d_delta;
   b.d_u = io->d_u;
+  b.dt_dd = dt_dd;
+  b.dt_du = dt_du;
   b.part_bc = static_cast<float*>(scr);
   b.part_par = reinterpret_cast<double*>(static_cast<char*>(scr) + pl.part_bc_bytes);
+  if (pl.pd_bytes > 0) {
+    // the first direction's sums in the workspace, behind the partials
+    b.pd_delta = reinterpret_cast<float*>(static_cast<char*>(scr) + pl.part_bc_bytes +
+                                          pl.part_par_bytes);
+    b.pd_u = b.pd_delta + a->B * a->L * a->D;
+  } else {
+    b.pd_delta = static_cast<float*>(io->d_delta);
+    b.pd_u = static_cast<float*>(io->d_u);
+  }
   b.bg = pl.bg;
   b.nbg = pl.nbg;
   b.tpw = pl.tpw;

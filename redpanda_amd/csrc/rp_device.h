@@ -210,6 +210,26 @@ __device__ __forceinline__ float round_storage(float v, int dtype) {
   return static_cast<float>(static_cast<_Float16>(v));
 }
 
+// A gradient element in its storage dtype at the byte offset o of its fp32
+// layout (o / 2 for a 16-bit one), rounded to nearest even as torch converts.
+__device__ __forceinline__ void store_grad(void* base, uint32_t o, float v, int dtype) {
+  if (dtype == RP_F32)
+    store_byte<float>(base, o, v);
+  else if (dtype == RP_BF16)
+    store_byte<uint16_t>(base, o >> 1, (uint16_t)(__float_as_uint(round_storage(v, RP_BF16)) >> 16));
+  else
+    store_byte<_Float16>(base, o >> 1, static_cast<_Float16>(v));
+}
+// The same at element index i.
+__device__ __forceinline__ void store_grad_at(void* base, int64_t i, float v, int dtype) {
+  if (dtype == RP_F32)
+    static_cast<float*>(base)[i] = v;
+  else if (dtype == RP_BF16)
+    static_cast<uint16_t*>(base)[i] = (uint16_t)(__float_as_uint(round_storage(v, RP_BF16)) >> 16);
+  else
+    static_cast<_Float16*>(base)[i] = static_cast<_Float16>(v);
+}
+
 // y * silu(z) as torch computes it: silu(z) = z / (1 + exp(-z)) rounded to
 // z's storage dtype, then the product in fp32.
 __device__ __forceinline__ float silu_gate(float y, float z, int dtype_z) {

@@ -47,8 +47,11 @@ struct BwdIO {
   const float* ckpt;
   const float* dh_last;     // (B, D, N) or null: gradient of the final h
   const float* dbeta_last;  // (B, D, N) or null: gradient of the final beta
-  float* d_delta;
-  float* d_u;
+  void* d_delta;     // (B, L, D) in dt_dd: written by the last direction
+  void* d_u;         // (B, L, D) in dt_du
+  float* pd_delta;   // (B, L, D) fp32: the first direction's sums, which the
+  float* pd_u;       //   second reads back (d_delta / d_u themselves when fp32)
+  int dt_dd, dt_du;  // storage codes of d_delta / d_u (RP_F32 unless asked)
   float* d_h0;       // (B, D, N) or null
   float* d_beta0;
   const float* dcache;  // (B, L, D) delta = softplus(x) cached by the forward (dsp only)

@@ -597,14 +597,14 @@ __device__ __forceinline__ void scan_bwd_tile(const ScanParams& p, const BwdIO& 
               const int e = tid + k * kThreads;
               if (dir == 1 && e < K * CB && e / CB < kcnt) {
                 const uint32_t o = oD[k] + (uint32_t)ch * stDY;
-                pdd[k][0] = load_byte<float>(io.d_delta, o);
-                pdd[k][1] = load_byte<float>(io.d_u, o);
+                pdd[k][0] = load_byte<float>(io.pd_delta, o);
+                pdd[k][1] = load_byte<float>(io.pd_u, o);
               }
             } else if (dir == 1) {
               const int64_t idx = dd_index(tid + k * kThreads, b, dir, i0, kcnt);
               if (idx >= 0) {
-                pdd[k][0] = io.d_delta[idx];
-                pdd[k][1] = io.d_u[idx];
+                pdd[k][0] = io.pd_delta[idx];
+                pdd[k][1] = io.pd_u[idx];
               }
             }
           }
@@ -824,8 +824,14 @@ __device__ __forceinline__ void scan_bwd_tile(const ScanParams& p, const BwdIO& 
                       const float2 v = dd_of(ONEBAR ? SL : 0, e / CB, e % CB, fdt[k], fuh[k]);
                       float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
                       if (p.dsp && dd_final(dir)) dd = fmul(dd, fsp[k]);
-                      store_byte<float>(io.d_delta, o, dd);
-                      store_byte<float>(io.d_u, o, dir == 0 ? v.y : pdd[k][1] + v.y);
+                      const float du = dir == 0 ? v.y : pdd[k][1] + v.y;
+                      if (dd_final(dir)) {
+                        store_grad(io.d_delta, o, dd, io.dt_dd);
+                        store_grad(io.d_u, o, du, io.dt_du);
+                      } else {
+                        store_byte<float>(io.pd_delta, o, dd);
+                        store_byte<float>(io.pd_u, o, du);
+                      }
                     }
                     continue;
                   }
@@ -835,8 +841,14 @@ __device__ __forceinline__ void scan_bwd_tile(const ScanParams& p, const BwdIO& 
                     float dd = dir == 0 ? v.x : pdd[k][0] + v.x;
                     // with softplus, the complete gradient is taken through it
                     if (p.dsp && dd_final(dir)) dd = fmul(dd, fsp[k]);
-                    io.d_delta[idx] = dd;
-                    io.d_u[idx] = dir == 0 ? v.y : pdd[k][1] + v.y;
+                    const float du = dir == 0 ? v.y : pdd[k][1] + v.y;
+                    if (dd_final(dir)) {
+                      store_grad_at(io.d_delta, idx, dd, io.dt_dd);
+                      store_grad_at(io.d_u, idx, du, io.dt_du);
+                    } else {
+                      io.pd_delta[idx] = dd;
+                      io.pd_u[idx] = du;
+                    }
                   }
                 }
               }

@@ -140,8 +140,12 @@ class _HipScan(torch.autograd.Function):
             dh_last = dh_last.to(torch.float32).contiguous()
         if dbeta_last is not None:
             dbeta_last = dbeta_last.to(torch.float32).contiguous()
-        d_delta = torch.empty((B, L, D), **f32)
-        d_u = torch.empty((B, L, D), **f32)
+        # d_delta and d_u leave the kernel in delta's and u's dtypes (rounded as
+        # torch converts), so 16-bit inputs need no conversion pass
+        if delta.dtype != torch.float32 or u.dtype != torch.float32:
+            args.grad_in_storage = 1
+        d_delta = torch.empty((B, L, D), dtype=delta.dtype, device=dev)
+        d_u = torch.empty((B, L, D), dtype=u.dtype, device=dev)
         d_B = torch.empty((B, L, N), **f32)
         d_C = torch.empty((B, L, N), **f32)
         d_Ar = torch.empty_like(Arc) if Arc is not None else None

@@ -44,9 +44,10 @@ def scan_fwd(c, bidirectional=False, with_ckpt=False, with_state=False, h0=None,
 
 
 def scan_fwd_bwd(c, bidirectional=False, dh_last=None, dbeta_last=None, h0=None, beta0=None,
-                 softplus=False):
+                 softplus=False, grad_in_storage=False):
     """Forward with checkpoints, then backward with upstream c['dy'] -> fp32 grads
-    (with an initial state h0, beta0 also its gradients, as grads 'h0' and 'beta0')."""
+    (with an initial state h0, beta0 also its gradients, as grads 'h0' and 'beta0';
+    with grad_in_storage, d_delta and d_u in delta's and u's dtypes)."""
     lib = _lib.load()
     y, ckpt, _, (a, keep) = scan_fwd(c, bidirectional, with_ckpt=True, h0=h0, beta0=beta0,
                                      softplus=softplus)
@@ -55,7 +56,10 @@ def scan_fwd_bwd(c, bidirectional=False, dh_last=None, dbeta_last=None, h0=None,
     N = Bc.shape[-1]
     f32 = dict(dtype=torch.float32, device="cuda")
     dy = _dev(c["dy"].float())
-    g = {"delta": torch.empty((B, L, D), **f32), "u": torch.empty((B, L, D), **f32),
+    a.grad_in_storage = 1 if grad_in_storage else 0
+    gdt = (delta.dtype, u.dtype) if grad_in_storage else (torch.float32, torch.float32)
+    g = {"delta": torch.empty((B, L, D), dtype=gdt[0], device="cuda"),
+         "u": torch.empty((B, L, D), dtype=gdt[1], device="cuda"),
          "Bc": torch.empty((B, L, N), **f32), "Cc": torch.empty((B, L, N), **f32),
          "Ar": None if Ar is None else torch.empty_like(Ar),
          "Ai": None if Ai is None else torch.empty_like(Ai),

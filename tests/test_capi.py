@@ -68,6 +68,7 @@ def test_valid_args_pass_check(lib):
     ("track", None, "track"),
     ("u_sl", -5, "stride"),
     ("delta_softplus", 2, "delta_softplus"),
+    ("grad_in_storage", 2, "grad_in_storage"),
 ])
 def test_invalid_scan_args_rejected(lib, field, value, needle):
     kw = {field: value}
@@ -110,6 +111,20 @@ def test_bwd_workspace_too_small_rejected(lib):
     io = _lib.ScanBwdIO(dy=f, ckpt=f, d_delta=f, d_u=f, d_Bc=f, d_Cc=f, d_A_real=f,
                         d_A_imag=f, d_track=f, work=f, work_bytes=16)
     assert lib.rp_scan_bwd(ctypes.byref(a), ctypes.byref(io), None) == -4
+
+
+def test_grad_in_storage_workspace(lib):
+    # 16-bit gradients of a bidirectional scan: the first direction's fp32
+    # (d_delta, d_u) sums join the workspace; causal scans write directly
+    base = lib.rp_scan_bwd_work_bytes(ctypes.byref(_good_args(bidirectional=1)))
+    wide = lib.rp_scan_bwd_work_bytes(ctypes.byref(_good_args(bidirectional=1, grad_in_storage=1)))
+    assert wide - base == 2 * (2 * 64 * 128) * 4
+    assert (lib.rp_scan_bwd_work_bytes(ctypes.byref(_good_args(grad_in_storage=1))) ==
+            lib.rp_scan_bwd_work_bytes(ctypes.byref(_good_args())))
+    f32 = dict(bidirectional=1, grad_in_storage=1, dtype_delta=_lib.RP_F32, dtype_u=_lib.RP_F32)
+    assert (lib.rp_scan_bwd_work_bytes(ctypes.byref(_good_args(**f32))) ==
+            lib.rp_scan_bwd_work_bytes(ctypes.byref(_good_args(bidirectional=1, dtype_delta=_lib.RP_F32,
+                                                               dtype_u=_lib.RP_F32))))
 
 
 def test_softplus_argument_checks(lib):

@@ -321,6 +321,43 @@ def test_backward_tile_walk_matches_single_tile(gpu_lib, D, bidir):
             assert e <= 1e-6, f"row {r} d{k}: {e:.2e}"
 
 
+@pytest.mark.parametrize("bidir", [False, True])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,L,D,NR,NT,softplus", [
+    (2, 37, 96, 32, 8, False),     # 8 lanes, whole tiles, a one-step last chunk
+    (3, 64, 100, 12, 4, True),     # 4 lanes, a partial tile, softplus on load
+    (2, 70, 64, 64, 8, False),     # 16 lanes
+    (1100, 9, 128, 64, 8, False),  # 16 lanes, 4 channel tiles per workgroup
+])
+def test_gradients_in_storage_dtype(gpu_lib, B, L, D, NR, NT, softplus, dtype, bidir):
+    """grad_in_storage: d_delta and d_u leave the backward in delta's and u's
+    16-bit dtype, rounded to nearest even: bit for bit torch's conversion of
+    the fp32 gradients that the default writes, every other output unchanged
+    (a bidirectional scan keeps its first direction's sums in the workspace)."""
+    c = make_case(900 + B + D, B=B, L=L, D=D, NR=NR, NT=NT, dtype=dtype)
+    if softplus:  # the dt projection x, softplus(x) ~ dt
+        c["delta"] = torch.log(torch.expm1(c["delta"].float())).to(dtype)
+    y0, g0 = hip_capi.scan_fwd_bwd(c, bidir, softplus=softplus)
+    y1, g1 = hip_capi.scan_fwd_bwd(c, bidir, softplus=softplus, grad_in_storage=True)
+    assert torch.equal(y0, y1)
+    assert g1["delta"].dtype == dtype and g1["u"].dtype == dtype
+    assert torch.equal(g1["delta"], g0["delta"].to(dtype))
+    assert torch.equal(g1["u"], g0["u"].to(dtype))
+    for k in ("Bc", "Cc", "Ar", "Ai", "Tk"):
+        assert (g0[k] is None and g1[k] is None) or torch.equal(g0[k], g1[k]), k
+
+
+def test_gradients_in_storage_dtype_mixed(gpu_lib):
+    """fp32 delta with bf16 u: d_delta stays fp32, d_u leaves in bf16."""
+    c = make_case(931, B=2, L=50, D=96, NR=32, NT=8, dtype=torch.bfloat16)
+    c["delta"] = c["delta"].float()
+    y0, g0 = hip_capi.scan_fwd_bwd(c, True)
+    y1, g1 = hip_capi.scan_fwd_bwd(c, True, grad_in_storage=True)
+    assert g1["delta"].dtype == torch.float32 and g1["u"].dtype == torch.bfloat16
+    assert torch.equal(g1["delta"], g0["delta"])
+    assert torch.equal(g1["u"], g0["u"].to(torch.bfloat16))
+
+
 def test_linearity_in_u(gpu_lib):
     scan, _ = _scan()
     c = make_case(501, B=2, L=40, D=64, NR=12, NT=4)
