@@ -22,7 +22,8 @@ dev = "cuda"
 
 
 def nrel(a, b):
-    return float((a.float() - b.float()).abs().max() / (b.float().abs().max() + 1e-30))
+    a, b = a.detach().float(), b.detach().float()
+    return float((a - b).abs().max() / (b.abs().max() + 1e-30))
 
 
 def _inputs(B, L, D, NR, NT, seed, dt=torch.float32):
