@@ -30,19 +30,23 @@ def _case(seed, B, L, D, NR, NT):
     return c
 
 
-def _backward(entry, c, bidirectional):
+def _backward(entry, c, bidirectional, in_storage=False):
     """Forward with checkpoints, then the backward through `entry`; every
     output the caller owns is allocated here, the scratch only by
-    rp_scan_bwd (a workspace) or not at all (rp_scan_bwd_noalloc)."""
+    rp_scan_bwd (a workspace) or not at all (rp_scan_bwd_noalloc).
+    in_storage: d_delta / d_u in the inputs' dtypes (grad_in_storage)."""
     lib = _lib.load()
     _, ckpt, _, (a, keep) = hip_capi.scan_fwd(c, bidirectional, with_ckpt=True)
-    _, u, Bc, Cc, Ar, Ai, Tk = keep[:7]
+    delta, u, Bc, Cc, Ar, Ai, Tk = keep[:7]
+    a.grad_in_storage = 1 if in_storage else 0
     B, L, D = u.shape
     N = Bc.shape[-1]
     f32 = dict(dtype=torch.float32, device="cuda")
     dy = c["dy"].to("cuda").contiguous()
-    g = {"delta": torch.full((B, L, D), float("nan"), **f32),
-         "u": torch.full((B, L, D), float("nan"), **f32),
+    g = {"delta": torch.full((B, L, D), float("nan"), dtype=delta.dtype if in_storage
+                             else torch.float32, device="cuda"),
+         "u": torch.full((B, L, D), float("nan"), dtype=u.dtype if in_storage else torch.float32,
+                         device="cuda"),
          "Bc": torch.full((B, L, N), float("nan"), **f32),
          "Cc": torch.full((B, L, N), float("nan"), **f32),
          "Ar": torch.full_like(Ar, float("nan")), "Ai": torch.full_like(Ai, float("nan")),
@@ -63,7 +67,8 @@ def _backward(entry, c, bidirectional):
 
 
 def _same_bits(x, y):
-    return all(torch.equal(x[k].view(torch.int32), y[k].view(torch.int32)) for k in x)
+    bits = lambda t: t.view(torch.int16 if t.element_size() == 2 else torch.int32)
+    return all(x[k].dtype == y[k].dtype and torch.equal(bits(x[k]), bits(y[k])) for k in x)
 
 
 def test_noalloc_equals_workspace_entry_twice(gpu_lib):
@@ -75,6 +80,24 @@ def test_noalloc_equals_workspace_entry_twice(gpu_lib):
               f"bidir={bidir}", flush=True)
         free = _backward("rp_scan_bwd_noalloc", c, bidir)
         ref = _backward("rp_scan_bwd", c, bidir)
+        assert all(torch.isfinite(v).all() for v in free.values())
+        assert _same_bits(free, ref)
+
+
+def test_noalloc_gradients_in_storage_dtype(gpu_lib):
+    """bf16 inputs with grad_in_storage: d_delta / d_u leave in bf16, and a
+    bidirectional scan keeps its first direction's fp32 sums in the static
+    scratch; two calls in a row, the second smaller, bit for bit
+    rp_scan_bwd's."""
+    to16 = lambda c: {k: (v.bfloat16() if k in ("delta", "u", "Bc", "Cc") else v)
+                      for k, v in c.items()}
+    for c, bidir in ((to16(_case(73, B=4, L=64, D=256, NR=32, NT=8)), True),
+                     (to16(_case(74, B=2, L=40, D=96, NR=12, NT=4)), True)):
+        print(f"case B={c['u'].shape[0]} L={c['u'].shape[1]} D={c['u'].shape[2]} bf16 "
+              f"bidir={bidir}", flush=True)
+        free = _backward("rp_scan_bwd_noalloc", c, bidir, in_storage=True)
+        ref = _backward("rp_scan_bwd", c, bidir, in_storage=True)
+        assert free["delta"].dtype == torch.bfloat16 and free["u"].dtype == torch.bfloat16
         assert all(torch.isfinite(v).all() for v in free.values())
         assert _same_bits(free, ref)
 
