@@ -67,6 +67,13 @@ STEP_SHAPE = dict(R=4096, layers=8, D=1024, NR=16, NT=4)
 # engine/search_mamba.py:28-35: 12 layers, d_model 384 -> d_inner 768,
 # d_state 32, no tracking states), 4096 rollouts.
 STEP_SHAPE_DEFAULT = dict(R=4096, layers=12, D=768, NR=32, NT=0)
+# The step kernel across state sizes (4096 rollouts, d_inner 1024, two
+# layers alternating so that neither block stays in the caches): (rotational,
+# tracking) splits from d_state 24 to 128, whole slots and pad states, the
+# last slot's split fixed at compile time or decided at run time.
+STEP_STATES = [(16, 8), (24, 4), (32, 0), (28, 8), (32, 8), (40, 4), (48, 0), (56, 4),
+               (64, 0), (64, 8), (64, 16), (80, 4), (96, 0), (90, 14), (100, 8), (112, 0),
+               (100, 16), (120, 8), (112, 16), (128, 0)]
 # Long-sequence causal stress: batch 64, L=2048, d_inner 1024, d_state 64
 # complex plus 8 tracking, fp32 inputs.
 LONG_SHAPE = dict(B=64, L=2048, D=1024, NR=64, NT=8)
@@ -95,6 +102,8 @@ def parse():
     ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer comparison")
     ap.add_argument("--no-mixer", action="store_true", help="skip the mixer-gate kernels")
     ap.add_argument("--no-rollout", action="store_true", help="skip the rollout-boundary ply")
+    ap.add_argument("--no-step-states", action="store_true",
+                    help="skip the step kernel across state sizes (d_state 24-128)")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the step sweep over rollout counts and the training-through-step "
                          "leg (their thousands of small launches swamp a kernel trace)")
@@ -1334,6 +1343,25 @@ def main():
         print(f"[bench] step {STEP_SHAPE_DEFAULT}: {step_def['t_launch'] * 1e6:.1f} us/launch, "
               f"{step_def['GBps']:.0f} GB/s; rank-1 cache {step_def['t_launch_rank1'] * 1e6:.1f} "
               f"us/launch, {step_def['GBps_rank1']:.0f} GB/s", file=sys.stderr, flush=True)
+    states = None
+    if not args.no_step and not args.no_step_states:
+        states = []
+        for NR, NT in STEP_STATES:
+            sh = dict(R=4096, layers=2, D=1024, NR=NR, NT=NT)
+            r = bench_step(torch, args, plies=16, shape=sh)
+            states.append({"d_state": NR + NT, "NR": NR, "NT": NT,
+                           "avg_launch_s": r["t_launch"], "alg_bytes_per_launch": r["bytes"],
+                           "achieved_GBps": r["GBps"], "frac": r["GBps"] / HBM_PEAK_GBS,
+                           "rank1_cache": {"avg_launch_s": r["t_launch_rank1"],
+                                           "alg_bytes_per_launch": r["bytes_rank1"],
+                                           "achieved_GBps": r["GBps_rank1"],
+                                           "frac": r["GBps_rank1"] / HBM_PEAK_GBS}})
+            print(f"[bench] step d_state {NR + NT:3d} ({NR}+{NT}): {r['t_launch'] * 1e6:7.1f} "
+                  f"us/launch, {r['GBps']:.0f} GB/s ({r['GBps'] / HBM_PEAK_GBS:.0%}); rank-1 "
+                  f"{r['t_launch_rank1'] * 1e6:7.1f} us, {r['GBps_rank1']:.0f} GB/s "
+                  f"({r['GBps_rank1'] / HBM_PEAK_GBS:.0%})", file=sys.stderr, flush=True)
+            del r
+            torch.cuda.empty_cache()
     lng = None
     if not args.no_long:
         print(f"[bench] long-sequence scan {LONG_SHAPE} fp32", file=sys.stderr, flush=True)
@@ -1484,6 +1512,10 @@ def main():
                             "(broadcast input state, no copies)",
                 "avg_launch_s": step["t_shared"], "alg_bytes_per_launch": step["bytes_shared"],
                 "achieved_GBps": step["GBps_shared"]},
+            "state_sizes": None if states is None else {
+                "workload": "the step kernel across state sizes: 4096 rollouts, d_inner 1024, "
+                            "two layers alternating, full and rank-1 caches",
+                "shapes": states},
             "search_model_default": {
                 "workload": "the step kernel at the reference's default search-model core "
                             "(SearchMambaConfig: 12 layers, d_inner 768, d_state 32 all "
