@@ -1038,6 +1038,8 @@ int rp_rmsnorm_fwd(const rp_rmsnorm_args* a, void* stream) {
 int rp_softplus(const float* x, float* out, int64_t n, void* stream) {
   if (n < 0) return fail(RP_ERR_INVALID, "softplus: n < 0");
   if (n > 0 && (x == nullptr || out == nullptr)) return fail(RP_ERR_INVALID, "softplus: NULL buffer");
+  if (n > 0 && (!aligned(x, 4) || !aligned(out, 4)))
+    return fail(RP_ERR_INVALID, "softplus: misaligned buffer");
   hipError_t e = rp::launch_softplus(x, out, n, (hipStream_t)stream);
   if (e != hipSuccess) return fail_hip(e, "softplus launch");
   return RP_OK;

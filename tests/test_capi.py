@@ -132,6 +132,8 @@ def test_softplus_argument_checks(lib):
     assert lib.rp_softplus(None, None, -1, None) < 0
     assert "n < 0" in lib.rp_last_error().decode()
     assert lib.rp_softplus(None, 0x10000, 8, None) < 0
+    assert lib.rp_softplus(0x10002, 0x10000, 8, None) < 0
+    assert "misaligned" in lib.rp_last_error().decode()
     assert lib.rp_softplus(None, None, 0, None) == 0
 
 
