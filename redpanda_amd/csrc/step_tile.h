@@ -88,7 +88,16 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   __shared__ float sBC[RIM][NBC * NP];    // B, C (B_prev) rows of the workgroup's rollouts
   // the (h, beta) block of one rollout: TCH channels x N states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NVM
-  __shared__ float4 sH[TCH * NV], sBt[TCH * NV];
+  // Rank-1 rows with pad states and 2 slices per thread (every vector tested
+  // at run time): the store-back of a vector past its row goes to a slot of
+  // its thread behind the block (kThreads float2s), so that no store sits
+  // behind a branch, and B_prev is read for every state, then selected.
+  // Not for the generic gate kind (no slot known rotational at compile
+  // time), whose registers it would take past three waves per SIMD, nor for
+  // full beta blocks, which move twice the bytes per update and gain nothing.
+  constexpr bool SINK = RANK1 && PAD && SS == 2 && GK::kRJ > 0;
+  constexpr int SINKV = SINK ? kThreads / 2 : 0;  // float4s of the sink
+  __shared__ float4 sH[TCH * NV + SINKV], sBt[TCH * NV];
   const int tid = threadIdx.x;
   const int tile = blockIdx.x % p.ctiles, rg = blockIdx.x / p.ctiles;
   const int c0 = tile * TCH;
@@ -257,7 +266,14 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       float& bs = (&b4[i / SS].x)[i % SS];
       // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
       // same bits as the product the full form stored (zero for a pad state)
-      const float hbp = RANK1 ? (in_row(j) ? fmul(hdp, Bp[n]) : 0.f) : 0.5f * bs;
+      float hbp;
+      if constexpr (SINK) {
+        // (a pad state's index stays in the row's LDS)
+        const float bpn = fmul(hdp, Bp[n]);
+        hbp = in_row(j) ? bpn : 0.f;
+      } else {
+        hbp = RANK1 ? (in_row(j) ? fmul(hdp, Bp[n]) : 0.f) : 0.5f * bs;
+      }
       const float g = gate_of<S, GK>(j, half * SS + ql, p.NR, has_imag, dt, pah[i], wh[i], sCos);
       const float hb = fmul(hd, Bs[n]);
       hs = ffma(g, hs, ffma(g, hbp, hb));  // fwd_update's form and rounding
@@ -283,7 +299,10 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     }
 #pragma unroll
     for (int v = 0; v < NVT; ++v) {
-      if (in_row(v)) {
+      if constexpr (SINK) {
+        const int k = in_row(v) ? cl * VPM + v * SPL + half : TCH * NV * 2 + tid;
+        sHv[k] = h4[v];
+      } else if (in_row(v)) {
         sHv[cl * VPM + v * SPL + half] = h4[v];
         if constexpr (!RANK1) sBv[cl * VPM + v * SPL + half] = b4[v];
       }
