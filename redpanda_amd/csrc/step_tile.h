@@ -89,12 +89,13 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   // the (h, beta) block of one rollout: TCH channels x N states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NVM
   // Rank-1 rows with pad states and 2 slices per thread (every vector tested
-  // at run time): the store-back of a vector past its row goes to a slot of
-  // its thread behind the block (kThreads float2s), so that no store sits
-  // behind a branch, and B_prev is read for every state, then selected.
-  // Not for the generic gate kind (no slot known rotational at compile
-  // time), whose registers it would take past three waves per SIMD, nor for
-  // full beta blocks, which move twice the bytes per update and gain nothing.
+  // at run time): B_prev is read for every state, then selected, and the
+  // store-back of a vector past its row goes to a slot of its thread behind
+  // the block (kThreads float2s), so that no LDS access sits behind a
+  // branch.  The sink not for the generic gate kind (no slot known
+  // rotational at compile time), whose registers it would take past three
+  // waves per SIMD, nor for full beta blocks, which move twice the bytes per
+  // update and gain nothing.
   constexpr bool SINK = RANK1 && PAD && SS == 2 && GK::kRJ > 0;
   constexpr int SINKV = SINK ? kThreads / 2 : 0;  // float4s of the sink
   __shared__ float4 sH[TCH * NV + SINKV], sBt[TCH * NV];
@@ -267,8 +268,8 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
       // same bits as the product the full form stored (zero for a pad state)
       float hbp;
-      if constexpr (SINK) {
-        // (a pad state's index stays in the row's LDS)
+      if constexpr (RANK1 && PAD && SS == 2) {
+        // (a pad state's index stays in the row's LDS; its B_prev is 0)
         const float bpn = fmul(hdp, Bp[n]);
         hbp = in_row(j) ? bpn : 0.f;
       } else {
