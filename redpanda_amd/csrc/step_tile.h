@@ -88,11 +88,11 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   __shared__ float sBC[RIM][NBC * NP];    // B, C (B_prev) rows of the workgroup's rollouts
   // the (h, beta) block of one rollout: TCH channels x N states each, as in
   // memory ([channel][state]), so float4 k holds channel k / NVM
-  // Rank-1 rows with pad states and 2 slices per thread (every vector tested
-  // at run time): B_prev is read for every state, then selected, and the
-  // store-back of a vector past its row goes to a slot of its thread behind
-  // the block (kThreads float2s), so that no LDS access sits behind a
-  // branch.  The sink not for the generic gate kind (no slot known
+  // Rank-1 rows with pad states: B_prev is read for every state, then
+  // selected (below); with 2 slices per thread (every vector tested at run
+  // time) the store-back of a vector past its row goes to a slot of its
+  // thread behind the block (kThreads float2s), so that no LDS access sits
+  // behind a branch.  The sink not for the generic gate kind (no slot known
   // rotational at compile time), whose registers it would take past three
   // waves per SIMD, nor for full beta blocks, which move twice the bytes per
   // update and gain nothing.
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
       // beta_prev / 2: from the full form, or (dt*u)_prev / 2 * B_prev, the
       // same bits as the product the full form stored (zero for a pad state)
       float hbp;
-      if constexpr (RANK1 && PAD && SS == 2) {
+      if constexpr (RANK1 && PAD) {
         // (a pad state's index stays in the row's LDS; its B_prev is 0)
         const float bpn = fmul(hdp, Bp[n]);
         hbp = in_row(j) ? bpn : 0.f;
