@@ -68,9 +68,9 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   // channel's states split between S / 4 adjacent lanes, 4 slices each (one
   // float4 per slot), so that the gate parameters and the states of a thread
   // fit the registers of several waves per SIMD (one thread per channel took
-  // 256 VGPRs, one wave per SIMD, at d_state 32 all rotational); at 8 slots
-  // of 16 (d_state 97-128) between S / 2 lanes, 2 slices each (one float2
-  // per slot)
+  // 256 VGPRs, one wave per SIMD, at d_state 32 all rotational); at 6 and 8
+  // slots of 16 (d_state 81-96, 97-128) between S / 2 lanes, 2 slices each
+  // (one float2 per slot)
   constexpr int SPL = step_tile_split(S, NPL);
   constexpr int SS = S / SPL;           // slices per thread
   constexpr int NPT = NP / SPL;         // states per thread
@@ -82,6 +82,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   constexpr int VPC = NP / SS;          // vectors per channel at N == NP
   constexpr int TCH = kThreads / SPL;   // channels per workgroup
   constexpr int NB = TCH * NV / kThreads;  // float4s per thread when staging a block (at most)
+  static_assert(TCH * NV % kThreads == 0, "a block stages in whole passes of the workgroup");
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
   constexpr int RIM = step_tile_ri_max(S, NPL, RANK1);  // rollouts per workgroup, at most
   __shared__ float2 sCos[kTab];           // (m, b (-sin a)) records of the gate table

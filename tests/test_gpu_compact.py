@@ -51,7 +51,13 @@ def _rank1_state(R, D, N, seed):
 SHAPES = [(300, 1024, 16, 4), (37, 200, 32, 8), (9, 96, 64, 8), (11, 130, 4, 2),
           (65, 384, 48, 16), (7, 100, 24, 8), (20, 192, 72, 8), (33, 256, 20, 8),
           (70, 512, 36, 8), (5, 64, 80, 10), (40, 256, 112, 16), (9, 70, 100, 16),
-          (6, 128, 100, 8)]
+          (6, 128, 100, 8),
+          # pad states at 8 slots of 16 with compile-time rotational slots
+          # (the branch-free rank-1 path), a run-time split there, and a
+          # partial tile; 6 slots (2 slices per thread); 4-slice pad shapes
+          (33, 256, 112, 0), (17, 128, 116, 8), (9, 96, 90, 14), (6, 100, 120, 8),
+          (12, 256, 80, 4), (7, 64, 88, 4), (5, 256, 96, 0), (11, 256, 64, 8),
+          (13, 256, 24, 4)]
 
 
 @pytest.mark.parametrize("R,D,NR,NT", SHAPES)
