@@ -199,12 +199,10 @@ constexpr int kStepTile = kThreads;
 // Threads per channel of the step tile kernel for S state slices: S / 4 from
 // 8 slices up (d_state 24-40 and 48-80), each thread taking 4 slices (one
 // float4 per slot); the tile then holds kStepTile / (S / 4) channels.
-// At 6 and 8 slots of 16 slices (d_state 81-96, 97-128) S / 2 threads of 2
-// slices each (one float2 per slot), halving a thread's states; not at 5,
-// where the 32-channel tile's 640 float4s would not stage in whole passes
-// of 256 threads.
+// From 5 slots of 16 slices up (d_state 65-128) S / 2 threads of 2 slices
+// each (one float2 per slot), halving a thread's states.
 constexpr int step_tile_split(int S, int NPL) {
-  return (S == 16 && (NPL == 6 || NPL == 8)) ? S / 2 : S >= 8 ? S / 4 : 1;
+  return (S == 16 && NPL >= 5) ? S / 2 : S >= 8 ? S / 4 : 1;
 }
 // Whether the step tile kernel takes the shape (S, NPL): d_state a multiple
 // of 4 up to S * NPL; below S * NPL the host also asks for pad states only

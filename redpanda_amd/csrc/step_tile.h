@@ -81,8 +81,9 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   static_assert(!PAD || SPL > 1, "a one-thread channel (S == 4) has no pad float4s");
   constexpr int VPC = NP / SS;          // vectors per channel at N == NP
   constexpr int TCH = kThreads / SPL;   // channels per workgroup
-  constexpr int NB = TCH * NV / kThreads;  // float4s per thread when staging a block (at most)
-  static_assert(TCH * NV % kThreads == 0, "a block stages in whole passes of the workgroup");
+  constexpr int NBLK = TCH * NV;      // float4s of a block at N == NP
+  constexpr int NB = (NBLK + kThreads - 1) / kThreads;  // float4s per thread when staging it (at most)
+  constexpr bool WHOLE = NBLK % kThreads == 0;  // whole passes of the workgroup; else the last is bounded
   constexpr int NBC = RANK1 ? 3 : 2;    // rows staged per rollout: B, C (and B_prev)
   constexpr int RIM = step_tile_ri_max(S, NPL, RANK1);  // rollouts per workgroup, at most
   __shared__ float2 sCos[kTab];           // (m, b (-sin a)) records of the gate table
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     return v < NVT - 1 || last_in;
   };
   // float4s of the block
-  const int nvalid = (FULLD && !PAD) ? TCH * NV : (FULLD ? TCH : min(TCH, p.D - c0)) * NVM;
+  const int nvalid = (FULLD && !PAD) ? NBLK : (FULLD ? TCH : min(TCH, p.D - c0)) * NVM;
   const bool has_imag = p.Ai != nullptr;
   const int r_lo = rg * p.ri;
   const int nr = min(p.R, r_lo + p.ri) - r_lo;  // <= RIM (checked by the host)
@@ -213,7 +214,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
       for (int m = 0; m < NB; ++m) {
         const int k = tid + m * kThreads;
-        if ((FULLD && !PAD) || k < nvalid) {
+        if ((FULLD && !PAD && WHOLE) || k < nvalid) {
           hl[m] = SHARED ? hi4[k] : load_stream(hi4 + k);
           if constexpr (!RANK1) bl[m] = SHARED ? bi4[k] : load_stream(bi4 + k);
         }
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
       for (int m = 0; m < NB; ++m) {
         const int k = tid + m * kThreads;
-        if ((FULLD && !PAD) || k < nvalid) {
+        if ((FULLD && !PAD && WHOLE) || k < nvalid) {
           sH[k] = hl[m];
           if constexpr (!RANK1) sBt[k] = bl[m];
         }
@@ -229,8 +230,10 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
     } else {
 #pragma unroll
       for (int m = 0; m < NB; ++m) {
-        sH[tid + m * kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (!RANK1) sBt[tid + m * kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (WHOLE || tid + m * kThreads < NBLK) {
+          sH[tid + m * kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if constexpr (!RANK1) sBt[tid + m * kThreads] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
       }
     }
     __syncthreads();  // the block (and, the first time, the table and B / C rows)
@@ -315,7 +318,7 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
 #pragma unroll
     for (int m = 0; m < NB; ++m) {
       const int k = tid + m * kThreads;
-      if ((FULLD && !PAD) || k < nvalid) {
+      if ((FULLD && !PAD && WHOLE) || k < nvalid) {
         store_stream(ho4 + k, sH[k]);
         if constexpr (!RANK1) store_stream(bo4 + k, sBt[k]);
       }

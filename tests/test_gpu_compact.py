@@ -57,7 +57,10 @@ SHAPES = [(300, 1024, 16, 4), (37, 200, 32, 8), (9, 96, 64, 8), (11, 130, 4, 2),
           # partial tile; 6 slots (2 slices per thread); 4-slice pad shapes
           (33, 256, 112, 0), (17, 128, 116, 8), (9, 96, 90, 14), (6, 100, 120, 8),
           (12, 256, 80, 4), (7, 64, 88, 4), (5, 256, 96, 0), (11, 256, 64, 8),
-          (13, 256, 24, 4)]
+          (13, 256, 24, 4),
+          # 5 slots of 16 (2 slices per thread, the block's last staging pass
+          # bounded): pad states in a middle slot, a partial tile
+          (10, 96, 56, 16), (3, 40, 60, 8), (8, 256, 72, 0)]
 
 
 @pytest.mark.parametrize("R,D,NR,NT", SHAPES)
