@@ -199,10 +199,11 @@ constexpr int kStepTile = kThreads;
 // Threads per channel of the step tile kernel for S state slices: S / 4 from
 // 8 slices up (d_state 24-40 and 48-80), each thread taking 4 slices (one
 // float4 per slot); the tile then holds kStepTile / (S / 4) channels.
-// From 5 slots of 16 slices up (d_state 65-128) S / 2 threads of 2 slices
-// each (one float2 per slot), halving a thread's states.
+// From 5 slots of 16 slices up (d_state 65-128), and at 5 slots of 8
+// (d_state 33-40), S / 2 threads of 2 slices each (one float2 per slot),
+// halving a thread's states.
 constexpr int step_tile_split(int S, int NPL) {
-  return (S == 16 && NPL >= 5) ? S / 2 : S >= 8 ? S / 4 : 1;
+  return ((S == 16 && NPL >= 5) || (S == 8 && NPL == 5)) ? S / 2 : S >= 8 ? S / 4 : 1;
 }
 // Whether the step tile kernel takes the shape (S, NPL): d_state a multiple
 // of 4 up to S * NPL; below S * NPL the host also asks for pad states only

@@ -60,7 +60,9 @@ SHAPES = [(300, 1024, 16, 4), (37, 200, 32, 8), (9, 96, 64, 8), (11, 130, 4, 2),
           (13, 256, 24, 4),
           # 5 slots of 16 (2 slices per thread, the block's last staging pass
           # bounded): pad states in a middle slot, a partial tile
-          (10, 96, 56, 16), (3, 40, 60, 8), (8, 256, 72, 0)]
+          (10, 96, 56, 16), (3, 40, 60, 8), (8, 256, 72, 0),
+          # 5 slots of 8 (2 slices per thread over 4 lanes, 64-channel tile)
+          (9, 128, 28, 8), (5, 100, 24, 12), (6, 64, 40, 0)]
 
 
 @pytest.mark.parametrize("R,D,NR,NT", SHAPES)
